@@ -1,0 +1,254 @@
+"""Benchmark of the SiQ-VL hot path on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+One step = one forward + backward of varlen packed attention over the config-2
+batch (Qwen2.5-1.5B heads: 12 q / 2 kv, d 128, 32 lognormal sequences, 16384
+tokens, causal), inputs already resident in HBM.  The headline ``value`` is
+its algorithmic TFLOP/s (12 * d * P * Hq per step, P = allowed (q, k) pairs of
+the realised cu_seqlens; recompute not counted).  The fused lm_head
+cross-entropy (config 4) is timed the same way and reported under ``ce``
+(tokens/s and TFLOP/s at 6 * n * hdim * vocab).
+
+Timing: HIP events recorded on the stream the kernels are launched on,
+bracketing K steps after W warm-up steps, with device synchronisation on both
+sides; per-call events give each operator's average duration for the
+roofline.  The CPU baseline times the reference path's own library calls
+(oracle/cpu_path.py: SDPA with a block-diagonal mask + repeat_kv, F.linear +
+F.cross_entropy, fp32 autograd) on a bounded sample of the same inputs.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+from siq_vl_amd import attention as A
+from siq_vl_amd import cross_entropy as C
+from siq_vl_amd import workloads as W
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CUs x 2.4 GHz)
+PEAK_HBM_GBS = 8000.0
+METRIC = "packed varlen attn fwd+bwd TFLOP/s (% bf16 MFMA peak); fused-CE tokens/s"
+
+
+def _events(n):
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def bench_attention(steps: int, warmup: int) -> dict:
+    cfg = W.attn_config(2)
+    dev = torch.device("cuda")
+    x = W.attn_inputs(cfg, device=dev)
+    cu = cfg.cu_seqlens().to(dev)
+    scale = cfg.d**-0.5
+    mx = cfg.max_seqlen
+
+    def step():
+        out, lse = A.varlen_attn_fwd(x["q"], x["k"], x["v"], cu, cu, mx, mx, scale, True)
+        dq, dk, dv = A.varlen_attn_bwd(x["dout"], x["q"], x["k"], x["v"], out, lse, cu, cu, mx, mx, scale, True)
+        return out, lse, dq, dk, dv
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = _events(3 * steps + 2)
+    # operator-level events: [fwd start, fwd end / bwd start, bwd end] per step
+    ev[0].record(stream)
+    for i in range(steps):
+        ev[1 + 3 * i].record(stream)
+        out, lse = A.varlen_attn_fwd(x["q"], x["k"], x["v"], cu, cu, mx, mx, scale, True)
+        ev[2 + 3 * i].record(stream)
+        A.varlen_attn_bwd(x["dout"], x["q"], x["k"], x["v"], out, lse, cu, cu, mx, mx, scale, True)
+        ev[3 + 3 * i].record(stream)
+    ev[-1].record(stream)
+    torch.cuda.synchronize()
+    total_ms = ev[0].elapsed_time(ev[-1])
+    fwd_ms = sorted(ev[1 + 3 * i].elapsed_time(ev[2 + 3 * i]) for i in range(steps))
+    bwd_ms = sorted(ev[2 + 3 * i].elapsed_time(ev[3 + 3 * i]) for i in range(steps))
+    med = lambda a: a[len(a) // 2]
+    pairs = cfg.pairs()
+    flops_fwd = 4.0 * cfg.d * pairs * cfg.hq
+    flops_bwd = 8.0 * cfg.d * pairs * cfg.hq
+    ms_step = total_ms / steps
+    # algorithmic bytes of one step: read q,k,v (fwd) + q,k,v,o,do,lse (bwd), write o,lse,dq,dk,dv
+    t, hq, hkv, d = cfg.total, cfg.hq, cfg.hkv, cfg.d
+    qb, kvb, lseb = t * hq * d * 2, t * hkv * d * 2, t * hq * 4
+    bytes_fwd = qb + 2 * kvb + qb + lseb
+    bytes_bwd = 3 * qb + 2 * kvb + lseb + qb + 2 * kvb
+    return {
+        "cfg": cfg,
+        "ms_per_step": ms_step,
+        "tflops": (flops_fwd + flops_bwd) / (ms_step * 1e-3) / 1e12,
+        "fwd_ms": med(fwd_ms),
+        "bwd_ms": med(bwd_ms),
+        "fwd_tflops": flops_fwd / (med(fwd_ms) * 1e-3) / 1e12,
+        "bwd_tflops": flops_bwd / (med(bwd_ms) * 1e-3) / 1e12,
+        "flops_bwd": flops_bwd,
+        "bytes": bytes_fwd + bytes_bwd,
+        "pairs": pairs,
+    }
+
+
+def bench_ce(steps: int, warmup: int, chunk: int) -> dict:
+    cfg = W.CONFIG4
+    dev = torch.device("cuda")
+    x = W.ce_inputs(cfg, device=dev)
+
+    def step():
+        return C.flce_fwd_bwd(x["hidden"], x["weight"], x["labels"], chunk_tokens=chunk)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = _events(steps + 1)
+    ev[0].record(stream)
+    for i in range(steps):
+        step()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    ms = ev[0].elapsed_time(ev[-1]) / steps
+    return {
+        "cfg": cfg,
+        "ms_per_step": ms,
+        "median_ms": per[len(per) // 2],
+        "tokens_per_s": cfg.n / (ms * 1e-3),
+        "tflops": cfg.flops() / (ms * 1e-3) / 1e12,
+        "chunk": chunk,
+    }
+
+
+def cpu_baseline(budget_s: float = 20.0) -> dict:
+    """Reference path (oracle/cpu_path.py) on the host cores, bounded sample."""
+    from oracle import cpu_path
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    res = {}
+    # attention: the first sequences of the config-2 batch, ~2048 tokens
+    cfg = W.attn_config(2)
+    lens = []
+    for n in cfg.lengths:
+        if sum(lens) + n > 2048 and lens:
+            break
+        lens.append(n)
+    x = W.attn_inputs(cfg, device="cpu", total=sum(lens))
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    q, k, v, do = (x[n].float().requires_grad_(n != "dout") for n in ("q", "k", "v", "dout"))
+    pairs = sum(n * (n + 1) // 2 for n in lens)
+    flops = 12.0 * cfg.d * pairs * cfg.hq
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        out = cpu_path.sdpa_attention(q, k, v, cu, cfg.d**-0.5, True)
+        out.backward(do)
+        reps += 1
+        if time.perf_counter() - t0 > budget_s / 2 or reps >= 50:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    res["attn"] = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+                   "kind": "port",
+                   "sample": f"config-2 first {len(lens)} sequences ({sum(lens)} tokens), fp32 SDPA + block-diagonal "
+                             f"mask + repeat_kv, fwd+bwd autograd, {reps} reps"}
+    # CE: 256 rows of config 4 against the full vocabulary
+    c4 = W.CONFIG4
+    g = torch.Generator().manual_seed(W.SEED)
+    n = 256
+    h = torch.randn(n, c4.hdim, generator=g).to(torch.bfloat16).float().requires_grad_(True)
+    w = (0.02 * torch.randn(c4.vocab, c4.hdim, generator=g)).to(torch.bfloat16).float().requires_grad_(True)
+    y = W.span_masked_labels(n, c4.vocab, c4.mask_frac, g)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        loss = cpu_path.cross_entropy(h, w, y)
+        loss.backward()
+        reps += 1
+        if time.perf_counter() - t0 > budget_s / 2 or reps >= 20:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    res["ce"] = {"value": n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+                 "sample": f"{n} rows of config 4 (hdim 1536, vocab 151936), F.linear + fp32 F.cross_entropy, "
+                           f"fwd+bwd autograd, {reps} reps"}
+    res["host"] = {"cpu_count": os.cpu_count(), "threads": torch.get_num_threads(), "cpu": platform.processor()}
+    return res
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ce-chunk", type=int, default=C.DEFAULT_CHUNK_TOKENS)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-ce", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+
+    att = bench_attention(args.steps, args.warmup)
+    print(f"[bench] attention fwd+bwd {att['ms_per_step']:.3f} ms/step, {att['tflops']:.1f} TFLOP/s "
+          f"(fwd {att['fwd_ms']:.3f} ms, bwd {att['bwd_ms']:.3f} ms)", file=sys.stderr, flush=True)
+    ce = None
+    if not args.skip_ce:
+        ce = bench_ce(max(3, args.steps // 4), min(args.warmup, 2), args.ce_chunk)
+        print(f"[bench] fused CE {ce['ms_per_step']:.3f} ms/step, {ce['tokens_per_s']:.3e} tokens/s, "
+              f"{ce['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu_baseline else cpu_baseline()
+
+    cfg = att["cfg"]
+    bwd_achieved = att["bwd_tflops"]
+    line = {
+        "metric": METRIC,
+        "value": round(att["tflops"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(att["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16, lognormal lengths; no checkpoint)",
+        "config": {"workload": "config 2: varlen causal GQA attention fwd+bwd, Qwen2.5-1.5B heads "
+                               "(12 q / 2 kv, d 128), 32 lognormal(400, 0.75) sequences, 16384 tokens",
+                   "total_tokens": cfg.total, "max_seqlen": cfg.max_seqlen, "pairs": att["pairs"],
+                   "pct_bf16_peak": round(100.0 * att["tflops"] / PEAK_BF16_TFLOPS, 2),
+                   "fwd_ms": round(att["fwd_ms"], 4), "bwd_ms": round(att["bwd_ms"], 4),
+                   "fwd_tflops": round(att["fwd_tflops"], 2), "bwd_tflops": round(att["bwd_tflops"], 2)},
+        "roofline": {"bound": "mfma", "kernel": "attention backward call (preprocess + dK/dV + dQ kernels)",
+                     "achieved": round(bwd_achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(bwd_achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": cpu["attn"] if cpu else None,
+    }
+    if ce is not None:
+        line["ce"] = {"workload": "config 4: fused linear CE fwd+bwd, h [16384,1536], W [151936,1536], 30% span mask",
+                      "tokens_per_s": round(ce["tokens_per_s"], 1), "ms_per_step": round(ce["ms_per_step"], 4),
+                      "tflops": round(ce["tflops"], 2),
+                      "pct_bf16_peak": round(100.0 * ce["tflops"] / PEAK_BF16_TFLOPS, 2),
+                      "chunk_tokens": ce["chunk"],
+                      "cpu_baseline": cpu["ce"] if cpu else None}
+    if cpu:
+        line["host"] = cpu["host"]
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

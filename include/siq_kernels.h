@@ -1,0 +1,136 @@
+/*
+ * siq_kernels.h -- C ABI of the SiQ-VL training hot path on MI355X (gfx950).
+ *
+ * Two operators, both hand-written HIP behind this plain-C boundary:
+ *   1. varlen (cu_seqlens-packed) flash attention, forward and backward,
+ *      causal GQA (Qwen2.5 decoder) or bidirectional (SigLIP tower);
+ *   2. fused lm_head linear + cross-entropy, forward and backward, without
+ *      materialising the [N, V] logits.
+ *
+ * Conventions
+ *  - Every entry point returns an int status (SIQ_OK = 0, < 0 on error) and
+ *    records a message readable with siq_last_error() (thread-local).
+ *  - All tensors are device pointers owned by the caller.  The library never
+ *    allocates, frees or keeps pointers beyond a call; scratch memory is the
+ *    caller's `workspace` (size from the matching *_workspace_bytes()).
+ *  - `stream` is a hipStream_t (NULL = the null stream).  Work is only
+ *    enqueued: no device synchronisation and no device-to-host reads.
+ *  - bf16 tensors are token-major: element (token t, head h, dim d) lives at
+ *    base + t * tok_stride + h * head_stride + d (d contiguous).  Base
+ *    pointers and both strides must keep 16-byte alignment (strides multiple
+ *    of 8 elements).
+ *  - cu_seqlens are int32 device arrays of batch+1 non-decreasing offsets with
+ *    cu[0] = 0 and cu[batch] = total.  They are read on the device; values
+ *    outside [0, total] are clamped there, so malformed offsets give wrong
+ *    numbers for the offending sequences but never an out-of-bounds access.
+ */
+#ifndef SIQ_KERNELS_H
+#define SIQ_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SIQ_ABI_VERSION 1
+
+enum siq_status {
+  SIQ_OK = 0,
+  SIQ_ERR_INVALID_ARGUMENT = -1, /* shape / dtype / value rejected before launch */
+  SIQ_ERR_UNSUPPORTED = -2,      /* e.g. head_dim not in {64, 128} */
+  SIQ_ERR_WORKSPACE = -3,        /* workspace missing or too small */
+  SIQ_ERR_ALIGNMENT = -4,        /* pointer or stride breaks 16-byte alignment */
+  SIQ_ERR_LAUNCH = -5            /* the HIP runtime rejected a launch */
+};
+
+/* Version of this ABI (SIQ_ABI_VERSION of the library that was built). */
+int siq_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* siq_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * Varlen attention.
+ *
+ * Replaces, for one packed batch, the attention call the reference reaches at
+ * transformers integrations/sdpa_attention.py:154-163 (F.scaled_dot_product_
+ * attention on a padded batch, reached from models/qwen2/modeling_qwen2.py:
+ * 216-230 and models/siglip/modeling_siglip.py:288-300) with the varlen
+ * contract of modeling_flash_attention_utils.py:796-822
+ * (q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+ * softmax_scale, causal).
+ *
+ * Shapes: q [total_q, hq, d], k/v [total_k, hkv, d], o like q, all bf16;
+ * lse fp32 [hq, total_q] (natural log, contiguous); hq % hkv == 0 and q-head h
+ * reads kv-head h / (hq / hkv); d in {64, 128}.  Causal masking is aligned
+ * bottom-right (q row i of a sequence sees k rows <= i + len_k - len_q), which
+ * is the usual top-left causal mask when len_q == len_k.
+ *
+ * strides[8] = {q_tok, q_head, k_tok, k_head, v_tok, v_head, o_tok, o_head}
+ * (in elements).
+ * ------------------------------------------------------------------------- */
+size_t siq_attn_fwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d);
+
+int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
+                        int max_seqlen_q, int max_seqlen_k, int64_t total_q, int64_t total_k, int hq, int hkv,
+                        int d, const int64_t* strides, float softmax_scale, int causal, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* Backward of siq_attn_varlen_fwd (the autograd backward of the same call in
+ * the reference path).  Inputs q, k, v, o, lse as produced/consumed by the
+ * forward, dout like o; outputs dq like q, dk/dv like k/v, each written in full
+ * (no accumulation).  Deterministic: no atomics, bitwise reproducible.
+ * strides[16] = {q_tok, q_head, k_tok, k_head, v_tok, v_head, o_tok, o_head,
+ *                do_tok, do_head, dq_tok, dq_head, dk_tok, dk_head, dv_tok, dv_head}. */
+size_t siq_attn_bwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d);
+
+int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                        const void* dout, void* dq, void* dk, void* dv, const int32_t* cu_seqlens_q,
+                        const int32_t* cu_seqlens_k, int batch, int max_seqlen_q, int max_seqlen_k,
+                        int64_t total_q, int64_t total_k, int hq, int hkv, int d, const int64_t* strides,
+                        float softmax_scale, int causal, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused linear cross-entropy (lm_head + loss), forward and backward.
+ *
+ * Replaces logits = lm_head(h) (transformers models/qwen2/modeling_qwen2.py:
+ * 465) followed by ForCausalLMLoss / fixed_cross_entropy (loss/loss_utils.py:
+ * 32-71: fp32 upcast, F.cross_entropy with ignore_index) and their autograd
+ * backward.  hidden [n, hdim] bf16 row-major, weight [vocab, hdim] bf16
+ * row-major, labels [n] int64 (already shifted; ignore_index rows are skipped;
+ * any other value outside [0, vocab) is treated as ignored and counted in
+ * *bad_labels).
+ *
+ * reduction 0 ("mean"): loss = sum_valid(lse - z_y) / count_valid.
+ * reduction 1 ("sum" then divide, as with num_items_in_batch):
+ *   loss = sum_valid(lse - z_y) / *divisor, divisor a device fp32 scalar.
+ * Outputs (device): *loss fp32 scalar, *count int64 number of valid rows,
+ * dhidden [n, hdim] bf16 = d loss / d hidden, dweight [vocab, hdim] bf16 =
+ * d loss / d weight (may be NULL to skip it).  Ignored rows get dhidden
+ * exactly 0.
+ *
+ * The logits are produced chunk_tokens rows at a time: only the softmax
+ * numerators of one chunk (chunk_tokens x vocab bf16, each relative to the max
+ * of its 256-column tile) ever exist, in the workspace.
+ * ------------------------------------------------------------------------- */
+size_t siq_flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk_tokens, int need_dweight);
+
+int siq_flce_fwd_bwd(const void* hidden, const void* weight, const int64_t* labels, int64_t n, int64_t hdim,
+                     int64_t vocab, int64_t ignore_index, int reduction, const float* divisor, float* loss,
+                     int64_t* count, int64_t* bad_labels, void* dhidden, void* dweight, int64_t chunk_tokens,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Multiplies a bf16 buffer in place by a device fp32 scalar (a no-op when the
+ * scalar is exactly 1.0): applies the upstream gradient of the scalar loss to
+ * dhidden / dweight.  Companion of siq_flce_fwd_bwd; no reference
+ * counterpart (autograd's chain rule). */
+int siq_scale_bf16_inplace(void* data, int64_t numel, const float* scalar, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SIQ_KERNELS_H */

@@ -1,0 +1,347 @@
+"""Varlen (cu_seqlens-packed) flash attention on MI355X: host side.
+
+Three layers, all ending in the HIP kernels behind ``include/siq_kernels.h``:
+
+* ``varlen_attn_fwd`` / ``varlen_attn_bwd`` -- raw operators (validation,
+  workspace, stream) over ``siq_attn_varlen_fwd`` / ``siq_attn_varlen_bwd``.
+* ``flash_attn_varlen_func`` -- the autograd op with the varlen call
+  convention transformers uses for packed batches
+  (transformers modeling_flash_attention_utils.py:796-822:
+  ``(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+  softmax_scale=..., causal=...)`` on ``[total, heads, dim]`` tensors).
+* ``siq_varlen_attention_forward`` -- the ``AttentionInterface`` function
+  (signature of transformers integrations/flash_attention.py:26-102), which the
+  reference's attention modules call at models/qwen2/modeling_qwen2.py:216-230
+  (causal GQA) and models/siglip/modeling_siglip.py:288-300 (bidirectional)
+  once ``config._attn_implementation == "siq_varlen"``.
+
+Semantics are those of the reference's eager/SDPA path
+(modeling_qwen2.py:138-172): fp32 softmax of ``scale * Q K^T`` plus the
+causal / padding mask, GQA with q-head ``h`` reading kv-head
+``h // (Hq // Hkv)``, output ``[B, S, Hq, D]``.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from . import _lib
+
+ATTN_IMPLEMENTATION = "siq_varlen"
+SUPPORTED_HEAD_DIMS = (64, 128)
+
+
+# --------------------------------------------------------------------------- validation
+def _check_token_major(name: str, t: torch.Tensor, heads: int | None = None, dim: int | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dim() != 3:
+        raise ValueError(f"{name} must be [total_tokens, heads, head_dim], got shape {tuple(t.shape)}")
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must live on the GPU, got device {t.device}")
+    if heads is not None and t.shape[1] != heads:
+        raise ValueError(f"{name} has {t.shape[1]} heads, expected {heads}")
+    if dim is not None and t.shape[2] != dim:
+        raise ValueError(f"{name} head_dim {t.shape[2]} != {dim}")
+    if t.stride(2) != 1:
+        raise ValueError(f"{name} must have a contiguous head_dim (stride(2) == 1)")
+    if t.shape[0] > 0 and (t.stride(0) % 8 or t.stride(1) % 8 or t.data_ptr() % 16):
+        raise ValueError(f"{name} rows must be 16-byte aligned (strides multiple of 8, aligned base)")
+
+
+def _ensure_token_major(t: torch.Tensor) -> torch.Tensor:
+    """Returns ``t`` if the kernels can read it in place, else a contiguous copy."""
+    if t.stride(2) == 1 and t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    return t.contiguous()
+
+
+def validate_cu_seqlens(cu: torch.Tensor, total: int, name: str = "cu_seqlens") -> None:
+    """Host-side checks on a CPU copy of cu_seqlens (the collator keeps one).
+
+    Rejects what the device path would silently clamp: wrong dtype or rank,
+    cu[0] != 0, decreasing offsets, cu[-1] != total.
+    """
+    if cu.dim() != 1 or cu.numel() < 1:
+        raise ValueError(f"{name} must be a 1-D tensor of batch+1 offsets")
+    if cu.dtype != torch.int32:
+        raise ValueError(f"{name} must be int32, got {cu.dtype}")
+    if cu.device.type != "cpu":
+        return
+    vals = cu.tolist()
+    if vals[0] != 0:
+        raise ValueError(f"{name}[0] must be 0, got {vals[0]}")
+    for a, b in zip(vals, vals[1:]):
+        if b < a:
+            raise ValueError(f"{name} must be non-decreasing ({a} then {b})")
+    if vals[-1] != total:
+        raise ValueError(f"{name}[-1] ({vals[-1]}) must equal the number of packed tokens ({total})")
+
+
+def _device_cu(cu: torch.Tensor, device: torch.device, total: int, name: str) -> torch.Tensor:
+    validate_cu_seqlens(cu, total, name)
+    if cu.device.type == "cpu":
+        cu = cu.to(device, non_blocking=False)
+    elif cu.device != device:
+        raise ValueError(f"{name} is on {cu.device}, expected {device} or the CPU")
+    return cu.contiguous()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_common(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> tuple[int, int, int]:
+    _check_token_major("q", q)
+    hq, d = q.shape[1], q.shape[2]
+    _check_token_major("k", k, dim=d)
+    hkv = k.shape[1]
+    _check_token_major("v", v, heads=hkv, dim=d)
+    if v.shape[0] != k.shape[0]:
+        raise ValueError(f"k and v token counts differ ({k.shape[0]} vs {v.shape[0]})")
+    if d not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim {d} unsupported (supported: {SUPPORTED_HEAD_DIMS})")
+    if hq % hkv:
+        raise ValueError(f"num q heads ({hq}) must be a multiple of num kv heads ({hkv})")
+    if not (q.device == k.device == v.device):
+        raise ValueError("q, k, v must be on the same device")
+    return hq, hkv, d
+
+
+# --------------------------------------------------------------------------- raw operators
+def varlen_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                    cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
+                    causal: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """Returns ``(out [total_q, hq, d] bf16, lse [hq, total_q] fp32, natural log)``."""
+    hq, hkv, d = _check_common(q, k, v)
+    total_q, total_k = q.shape[0], k.shape[0]
+    cu_q = _device_cu(cu_seqlens_q, q.device, total_q, "cu_seqlens_q")
+    cu_k = _device_cu(cu_seqlens_k, q.device, total_k, "cu_seqlens_k")
+    if cu_q.numel() != cu_k.numel():
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must describe the same number of sequences")
+    batch = cu_q.numel() - 1
+    out = torch.empty((total_q, hq, d), dtype=q.dtype, device=q.device)
+    lse = torch.empty((hq, total_q), dtype=torch.float32, device=q.device)
+    L = _lib.lib()
+    ws_bytes = L.siq_attn_fwd_workspace_bytes(batch, total_q, total_k, hq, hkv, d)
+    ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=q.device)
+    strides = _lib.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+                                out.stride(0), out.stride(1)])
+    rc = L.siq_attn_varlen_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                               cu_q.data_ptr(), cu_k.data_ptr(), batch, int(max_seqlen_q), int(max_seqlen_k),
+                               total_q, total_k, hq, hkv, d, strides, float(softmax_scale), int(bool(causal)),
+                               ws.data_ptr(), ws.numel(), _stream(q.device))
+    _lib.check(rc, "siq_attn_varlen_fwd")
+    return out, lse
+
+
+def varlen_attn_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                    lse: torch.Tensor, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
+                    max_seqlen_k: int, softmax_scale: float,
+                    causal: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Returns ``(dq, dk, dv)``, bitwise deterministic."""
+    hq, hkv, d = _check_common(q, k, v)
+    total_q, total_k = q.shape[0], k.shape[0]
+    _check_token_major("out", out, heads=hq, dim=d)
+    _check_token_major("dout", dout, heads=hq, dim=d)
+    if out.shape[0] != total_q or dout.shape[0] != total_q:
+        raise ValueError("out / dout must have total_q rows")
+    if lse.shape != (hq, total_q) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError(f"lse must be a contiguous fp32 [{hq}, {total_q}] tensor")
+    cu_q = _device_cu(cu_seqlens_q, q.device, total_q, "cu_seqlens_q")
+    cu_k = _device_cu(cu_seqlens_k, q.device, total_k, "cu_seqlens_k")
+    batch = cu_q.numel() - 1
+    dq = torch.empty((total_q, hq, d), dtype=q.dtype, device=q.device)
+    dk = torch.empty((total_k, hkv, d), dtype=q.dtype, device=q.device)
+    dv = torch.empty((total_k, hkv, d), dtype=q.dtype, device=q.device)
+    L = _lib.lib()
+    ws_bytes = L.siq_attn_bwd_workspace_bytes(batch, total_q, total_k, hq, hkv, d)
+    ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=q.device)
+    strides = _lib.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+                                out.stride(0), out.stride(1), dout.stride(0), dout.stride(1), dq.stride(0),
+                                dq.stride(1), dk.stride(0), dk.stride(1), dv.stride(0), dv.stride(1)])
+    rc = L.siq_attn_varlen_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                               dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), cu_q.data_ptr(),
+                               cu_k.data_ptr(), batch, int(max_seqlen_q), int(max_seqlen_k), total_q, total_k, hq,
+                               hkv, d, strides, float(softmax_scale), int(bool(causal)), ws.data_ptr(), ws.numel(),
+                               _stream(q.device))
+    _lib.check(rc, "siq_attn_varlen_bwd")
+    return dq, dk, dv
+
+
+class _VarlenAttnFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, scale, causal):
+        q, k, v = (_ensure_token_major(t) for t in (q, k, v))
+        cu_q = _device_cu(cu_q, q.device, q.shape[0], "cu_seqlens_q")
+        cu_k = _device_cu(cu_k, q.device, k.shape[0], "cu_seqlens_k")
+        out, lse = varlen_attn_fwd(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal)
+        ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k)
+        ctx.args = (max_q, max_k, scale, causal)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse, cu_q, cu_k = ctx.saved_tensors
+        max_q, max_k, scale, causal = ctx.args
+        dout = _ensure_token_major(dout)
+        dq, dk, dv = varlen_attn_bwd(dout, q, k, v, out, lse, cu_q, cu_k, max_q, max_k, scale, causal)
+        return dq, dk, dv, None, None, None, None, None, None
+
+
+def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                           cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int, dropout_p: float = 0.0,
+                           softmax_scale: float | None = None, causal: bool = False,
+                           window_size: tuple[int, int] = (-1, -1), softcap: float = 0.0,
+                           alibi_slopes: torch.Tensor | None = None, deterministic: bool = True,
+                           return_attn_probs: bool = False, **kwargs: Any) -> torch.Tensor:
+    """Varlen attention with the flash-attention varlen call convention.
+
+    ``q [total_q, hq, d]``, ``k/v [total_k, hkv, d]`` (bf16); returns ``[total_q, hq, d]``.
+    Features outside the reference path (dropout, sliding window, softcap,
+    ALiBi, returning probabilities) are rejected, not approximated.
+    """
+    if dropout_p:
+        raise ValueError("siq_varlen attention does not implement dropout (the reference trains with dropout 0)")
+    if tuple(window_size) != (-1, -1):
+        raise ValueError("sliding-window attention is not supported")
+    if softcap:
+        raise ValueError("logit softcapping is not supported")
+    if alibi_slopes is not None:
+        raise ValueError("ALiBi is not supported")
+    if return_attn_probs:
+        raise ValueError("attention probabilities are never materialised")
+    if softmax_scale is None:
+        softmax_scale = q.shape[-1] ** -0.5
+    return _VarlenAttnFn.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), int(max_seqlen_k),
+                               float(softmax_scale), bool(causal))
+
+
+# --------------------------------------------------------------------------- transformers plug-in
+def _cu_from_position_ids(position_ids: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """Packed position_ids restart at 0 for each sequence (transformers
+    modeling_flash_attention_utils.py:458-495): offsets are where they do."""
+    pos = position_ids.reshape(-1)
+    starts = torch.nonzero(pos == 0, as_tuple=False).reshape(-1).to(torch.int32)
+    if starts.numel() == 0 or int(starts[0]) != 0:
+        starts = torch.cat([torch.zeros(1, dtype=torch.int32, device=pos.device), starts])
+    total = torch.tensor([pos.numel()], dtype=torch.int32, device=pos.device)
+    cu = torch.cat([starts, total])
+    max_len = int((cu[1:] - cu[:-1]).max().item())
+    return cu, max_len
+
+
+def siq_varlen_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: torch.Tensor,
+                                 value: torch.Tensor, attention_mask: torch.Tensor | None, dropout: float = 0.0,
+                                 scaling: float | None = None, sliding_window: int | None = None,
+                                 softcap: float | None = None, is_causal: bool | None = None,
+                                 **kwargs: Any) -> tuple[torch.Tensor, None]:
+    """``AttentionInterface`` entry: ``query [B, Hq, S, D]``, ``key/value [B, Hkv, S, D]``
+    -> ``(out [B, S, Hq, D] contiguous, None)``.
+
+    Packing is read, in order, from ``cu_seq_lens_q/k`` + ``max_length_q/k``
+    kwargs, from restarting ``position_ids`` (B == 1), or from a 2-D padding
+    ``attention_mask`` (rows are unpadded); otherwise every batch row is one
+    sequence.  Unknown kwargs (e.g. the collator's raw ``questions``) are
+    ignored.
+    """
+    if dropout:
+        raise ValueError("siq_varlen attention does not implement dropout")
+    if softcap:
+        raise ValueError("logit softcapping is not supported")
+    if sliding_window is not None:
+        raise ValueError("sliding-window attention is not supported")
+    if is_causal is None:
+        is_causal = bool(getattr(module, "is_causal", False))
+    bsz, hq, s_q, d = query.shape
+    hkv, s_k = key.shape[1], key.shape[2]
+    if scaling is None:
+        scaling = d**-0.5
+    target = query.dtype if query.dtype == torch.bfloat16 else torch.bfloat16
+    q = query.transpose(1, 2).to(target)
+    k = key.transpose(1, 2).to(target)
+    v = value.transpose(1, 2).to(target)
+
+    cu_q = kwargs.get("cu_seq_lens_q")
+    cu_k = kwargs.get("cu_seq_lens_k")
+    max_q = kwargs.get("max_length_q")
+    max_k = kwargs.get("max_length_k")
+    position_ids = kwargs.get("position_ids")
+    if cu_q is not None and cu_k is not None and max_q is not None and max_k is not None:
+        out = flash_attn_varlen_func(q.reshape(-1, hq, d), k.reshape(-1, hkv, d), v.reshape(-1, hkv, d),
+                                     cu_q.to(torch.int32), cu_k.to(torch.int32), int(max_q), int(max_k),
+                                     softmax_scale=scaling, causal=is_causal)
+        out = out.reshape(bsz, s_q, hq, d)
+    elif attention_mask is not None and attention_mask.dim() == 2:
+        mask = attention_mask[:, -s_k:].to(torch.bool)
+        seqlens = mask.sum(dim=-1, dtype=torch.int32)
+        cu = torch.nn.functional.pad(torch.cumsum(seqlens, 0, dtype=torch.int32), (1, 0))
+        idx = torch.nonzero(mask.reshape(-1), as_tuple=False).reshape(-1)
+        maxlen = int(seqlens.max().item())
+        if s_q != s_k:
+            raise ValueError("padded (unpacked) inputs need equal query and key lengths")
+        qu = q.reshape(-1, hq, d).index_select(0, idx)
+        ku = k.reshape(-1, hkv, d).index_select(0, idx)
+        vu = v.reshape(-1, hkv, d).index_select(0, idx)
+        ou = flash_attn_varlen_func(qu, ku, vu, cu, cu, maxlen, maxlen, softmax_scale=scaling, causal=is_causal)
+        out = torch.zeros((bsz * s_q, hq, d), dtype=ou.dtype, device=ou.device)
+        out = out.index_copy(0, idx, ou).reshape(bsz, s_q, hq, d)
+    elif position_ids is not None and bsz == 1 and s_q == s_k:
+        cu, maxlen = _cu_from_position_ids(position_ids)
+        out = flash_attn_varlen_func(q.reshape(-1, hq, d), k.reshape(-1, hkv, d), v.reshape(-1, hkv, d), cu, cu,
+                                     maxlen, maxlen, softmax_scale=scaling, causal=is_causal)
+        out = out.reshape(bsz, s_q, hq, d)
+    else:
+        if attention_mask is not None:
+            raise ValueError("siq_varlen expects a 2-D padding mask or None (register its mask interface)")
+        cu_q = torch.arange(0, (bsz + 1) * s_q, s_q, dtype=torch.int32, device=query.device)
+        cu_k = torch.arange(0, (bsz + 1) * s_k, s_k, dtype=torch.int32, device=query.device)
+        out = flash_attn_varlen_func(q.reshape(-1, hq, d), k.reshape(-1, hkv, d), v.reshape(-1, hkv, d), cu_q, cu_k,
+                                     s_q, s_k, softmax_scale=scaling, causal=is_causal)
+        out = out.reshape(bsz, s_q, hq, d)
+    return out.to(query.dtype).contiguous(), None
+
+
+def register(name: str = ATTN_IMPLEMENTATION) -> str:
+    """Registers the kernels as a transformers attention backend.
+
+    After this, ``from_pretrained(..., attn_implementation="siq_varlen")`` (the
+    reference's model builders at siq_vl/model/modeling.py:326-327,363) or
+    ``config._attn_implementation = "siq_varlen"`` routes every Qwen2 / SigLIP
+    attention call here.  The mask interface is the flash-attention one: the
+    function receives ``None`` or a 2-D padding mask, never a 4-D bias.
+    """
+    from transformers import AttentionInterface
+
+    AttentionInterface.register(name, siq_varlen_attention_forward)
+    try:
+        from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, flash_attention_mask
+
+        ALL_MASK_ATTENTION_FUNCTIONS.register(name, flash_attention_mask)
+    except ImportError:  # older transformers: masks are resolved by name
+        pass
+    return name
+
+
+def attention_flops(cu_seqlens: torch.Tensor, hq: int, d: int, causal: bool, backward: bool = True) -> float:
+    """Algorithmic FLOPs: 4*D*P*Hq forward (+ 8*D*P*Hq backward), P = allowed
+    (q, k) pairs of the realised cu_seqlens; recompute is not counted."""
+    lens = (cu_seqlens[1:] - cu_seqlens[:-1]).to(torch.float64).cpu()
+    pairs = float((lens * (lens + 1) / 2).sum()) if causal else float((lens * lens).sum())
+    return (12.0 if backward else 4.0) * d * pairs * hq
+
+
+__all__ = [
+    "ATTN_IMPLEMENTATION",
+    "attention_flops",
+    "flash_attn_varlen_func",
+    "register",
+    "siq_varlen_attention_forward",
+    "validate_cu_seqlens",
+    "varlen_attn_bwd",
+    "varlen_attn_fwd",
+]

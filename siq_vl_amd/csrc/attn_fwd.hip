@@ -1,0 +1,185 @@
+// Varlen (cu_seqlens-packed) flash attention forward for gfx950.
+//
+// Semantics follow the reference path's eager definition
+// (transformers models/qwen2/modeling_qwen2.py:150-172, siglip
+// modeling_siglip.py:227-247): O = softmax(scale * Q K^T + mask) V per
+// sequence, fp32 softmax, GQA with q-head h reading kv-head h / (Hq / Hkv)
+// (repeat_kv, modeling_qwen2.py:138-147); causal masking is bottom-right
+// aligned as in the flash-attention varlen contract
+// (modeling_flash_attention_utils.py:796-822), identical to top-left when
+// len_q == len_k.  Also writes the natural-log LSE the backward needs.
+//
+// One workgroup = 4 waves = 128 q rows of one q-head of one sequence; the
+// (sequence, q-tile) comes from the device-side schedule (heaviest first).
+// Each wave owns 32 q rows and keeps its Q fragment in registers as the B
+// operand of S^T = K Q^T (v_mfma_f32_32x32x16_bf16), so each lane ends up
+// holding 16 scores of ONE q row: the online-softmax max/sum is in-lane plus
+// one cross-half swap.  P^T then feeds O^T += V^T P^T directly from registers.
+// K (row-major) and V (transposed) tiles of 64 kv rows are double-buffered in
+// LDS; the next tile's global loads are in flight while the current one is
+// multiplied.
+#include "attn.h"
+
+namespace siq {
+
+namespace {
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnParams p) {
+  constexpr int BM = kFwdBM, BN = kFwdBN, NT = 256;
+  using KTile = Tile4x8<BN, D, NT, false>;
+  using VTile = Tile4x8<BN, D, NT, true>;
+  constexpr int KS = KTile::RS, VS = VTile::TS;
+  constexpr int KSZ = BN * KS, VSZ = D * VS, STAGE = KSZ + VSZ;
+  __shared__ __align__(16) bf16 smem[2 * STAGE];
+
+  const int2 tl = p.qtiles[blockIdx.x];
+  if (tl.x < 0) return;
+  const SeqInfo si = p.seq[tl.x];
+  const int hqi = blockIdx.y, hk = hqi / p.n_rep;
+  const int q0 = tl.y * BM;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int off = si.k_len - si.q_len;
+  int kv_end = si.k_len;
+  if (CAUSAL) kv_end = min(kv_end, q0 + BM + off);
+  const int nblk = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
+
+  const int qrow = q0 + 32 * w + l32;
+  const bool qvalid = qrow < si.q_len;
+  bf16x8 qf[D / 16];
+  {
+    const bf16* qp = p.q + (int64_t)(si.q_start + (qvalid ? qrow : 0)) * p.q_tok + (int64_t)hqi * p.q_head + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) qf[ks] = qvalid ? ld_bf16x8(qp + 16 * ks) : zero_bf16x8();
+  }
+  f32x16 oacc[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) oacc[i] = zero16();
+  float mrow = -INFINITY, lsum = 0.f;  // running max in log2 units, per-half partial sum
+  const float c = p.scale_log2;
+
+  const bf16* kbase = p.k + (int64_t)si.k_start * p.k_tok + (int64_t)hk * p.k_head;
+  const bf16* vbase = p.v + (int64_t)si.k_start * p.v_tok + (int64_t)hk * p.v_head;
+  KTile kt;
+  VTile vt;
+  if (nblk > 0) {
+    kt.load(kbase, p.k_tok, si.k_len, tid);
+    vt.load(vbase, p.v_tok, si.k_len, tid);
+    kt.store_rows(smem, tid);
+    vt.store_cols(smem + KSZ, tid);
+  }
+  __syncthreads();
+
+  const int wq_last = q0 + 32 * w + 31;  // last q row of this wave
+  for (int kb = 0; kb < nblk; ++kb) {
+    const bf16* Ks = smem + (kb & 1) * STAGE;
+    const bf16* Vt = Ks + KSZ;
+    const int k0 = kb * BN;
+    const bool more = kb + 1 < nblk;
+    if (more) {
+      kt.load(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN, tid);
+      vt.load(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN, tid);
+    }
+    const bool active = !CAUSAL || (k0 <= wq_last + off);
+    if (active) {
+      f32x16 s[BN / 32];
+#pragma unroll
+      for (int t = 0; t < BN / 32; ++t) {
+        s[t] = zero16();
+        const bf16* kr = Ks + (32 * t + perm32(l32)) * KS + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks) s[t] = mfma32(ld_bf16x8(kr + 16 * ks), qf[ks], s[t]);
+      }
+      const bool need_mask = (k0 + BN > si.k_len) || (CAUSAL && k0 + BN - 1 > q0 + 32 * w + off);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < BN / 32; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = s[t][r] * c;
+          if (need_mask) {
+            const int kv = k0 + 32 * t + drow(r, h);
+            if (kv >= si.k_len || (CAUSAL && kv > qrow + off)) x = -INFINITY;
+          }
+          s[t][r] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+      mx = wave_max_xor32(mx);
+      const float mnew = fmaxf(mrow, mx);
+      const float msafe = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = exp2f_fast(mrow - msafe);
+      mrow = mnew;
+      lsum *= alpha;
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i) oacc[i] *= alpha;
+      float ps = 0.f;
+#pragma unroll
+      for (int t = 0; t < BN / 32; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = exp2f_fast(s[t][r] - msafe);
+          s[t][r] = e;
+          ps += e;
+        }
+      }
+      lsum += ps;
+      bf16x8 pb[BN / 16];
+#pragma unroll
+      for (int t = 0; t < BN / 32; ++t) {
+        pb[2 * t] = pack8(s[t], 0);
+        pb[2 * t + 1] = pack8(s[t], 8);
+      }
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const bf16* vr = Vt + (32 * dt + perm32(l32)) * VS + 8 * h;
+#pragma unroll
+        for (int st = 0; st < BN / 16; ++st) oacc[dt] = mfma32(ld_bf16x8(vr + 16 * st), pb[st], oacc[dt]);
+      }
+    }
+    if (more) {
+      bf16* nx = smem + ((kb + 1) & 1) * STAGE;
+      kt.store_rows(nx, tid);
+      vt.store_cols(nx + KSZ, tid);
+    }
+    __syncthreads();
+  }
+
+  const float ltot = wave_sum_xor32(lsum);
+  if (qvalid) {
+    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    bf16* op = p.out + (int64_t)(si.q_start + qrow) * p.o_tok + (int64_t)hqi * p.o_head;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        bf16x8 ov;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ov[i] = (bf16)(oacc[dt][8 * j + i] * inv);
+        st_bf16x8(op + 32 * dt + 16 * j + 8 * h, ov);
+      }
+    }
+    if (h == 0) {
+      p.lse[(int64_t)hqi * p.lse_head + si.q_start + qrow] =
+          ltot > 0.f ? (mrow + __log2f(ltot)) * kLn2 : -INFINITY;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_attn_fwd(const AttnParams& p, int d, int causal, int qcap, hipStream_t stream) {
+  const dim3 grid(qcap, p.hq), block(256);
+  if (d == 128) {
+    if (causal) hipLaunchKernelGGL((attn_fwd_kernel<128, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((attn_fwd_kernel<128, false>), grid, block, 0, stream, p);
+  } else if (d == 64) {
+    if (causal) hipLaunchKernelGGL((attn_fwd_kernel<64, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((attn_fwd_kernel<64, false>), grid, block, 0, stream, p);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace siq

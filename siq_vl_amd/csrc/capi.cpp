@@ -1,0 +1,298 @@
+// extern "C" boundary: host-side validation, workspace carving, launches.
+// Every check here happens before anything is enqueued, so a rejected call
+// leaves the stream untouched.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/siq_kernels.h"
+#include "attn.h"
+#include "flce.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return SIQ_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct AttnLayout {
+  size_t seq, qtiles, kvtiles, delta, total;
+  int qcap, kvcap;
+};
+
+AttnLayout attn_layout(int batch, int64_t total_q, int64_t total_k, int hq, bool bwd) {
+  AttnLayout L{};
+  L.qcap = (int)siq::tile_cap(total_q, batch, siq::kFwdBM);
+  L.kvcap = bwd ? (int)siq::tile_cap(total_k, batch, siq::kBwdBN) : 0;
+  size_t off = 0;
+  L.seq = off;
+  off += align256(sizeof(siq::SeqInfo) * (size_t)(batch > 0 ? batch : 1));
+  L.qtiles = off;
+  off += align256(sizeof(int2) * (size_t)L.qcap);
+  L.kvtiles = off;
+  off += align256(sizeof(int2) * (size_t)L.kvcap);
+  L.delta = off;
+  if (bwd) off += align256(sizeof(float) * (size_t)hq * (size_t)total_q);
+  L.total = off;
+  return L;
+}
+
+int check_attn_common(int batch, int max_q, int max_k, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
+                      float scale, const void* cu_q, const void* cu_k) {
+  if (batch < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "batch must be >= 0 (got %d)", batch);
+  if (total_q < 0 || total_k < 0 || total_q >= (int64_t(1) << 31) || total_k >= (int64_t(1) << 31))
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "total_q/total_k must be in [0, 2^31) (got %lld, %lld)",
+                (long long)total_q, (long long)total_k);
+  if (max_q < 0 || max_k < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "max_seqlen must be >= 0");
+  if (hq <= 0 || hkv <= 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "head counts must be positive (hq=%d, hkv=%d)", hq, hkv);
+  if (hq % hkv != 0)
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "hq (%d) must be a multiple of hkv (%d) for GQA", hq, hkv);
+  if (d != 64 && d != 128) return fail(SIQ_ERR_UNSUPPORTED, "head_dim %d unsupported (64 or 128)", d);
+  if (!std::isfinite(scale)) return fail(SIQ_ERR_INVALID_ARGUMENT, "softmax_scale must be finite");
+  if (batch > 0 && (cu_q == nullptr || cu_k == nullptr))
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "cu_seqlens_q / cu_seqlens_k must not be NULL");
+  return SIQ_OK;
+}
+
+int check_tensor(const char* name, const void* p, const int64_t* st, bool need) {
+  if (!need) return SIQ_OK;
+  if (p == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "%s must not be NULL", name);
+  if (!aligned16(p)) return fail(SIQ_ERR_ALIGNMENT, "%s is not 16-byte aligned", name);
+  if (st[0] < 0 || st[1] < 0 || (st[0] & 7) || (st[1] & 7))
+    return fail(SIQ_ERR_ALIGNMENT, "%s strides (%lld, %lld) must be non-negative multiples of 8 elements", name,
+                (long long)st[0], (long long)st[1]);
+  return SIQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int siq_abi_version(void) { return SIQ_ABI_VERSION; }
+
+const char* siq_last_error(void) { return g_last_error.c_str(); }
+
+size_t siq_attn_fwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d) {
+  (void)hkv;
+  (void)d;
+  if (batch < 0 || total_q < 0 || total_k < 0 || hq <= 0) return 0;
+  return attn_layout(batch, total_q, total_k, hq, false).total;
+}
+
+size_t siq_attn_bwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d) {
+  (void)hkv;
+  (void)d;
+  if (batch < 0 || total_q < 0 || total_k < 0 || hq <= 0) return 0;
+  return attn_layout(batch, total_q, total_k, hq, true).total;
+}
+
+int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, float* lse, const int32_t* cu_q,
+                        const int32_t* cu_k, int batch, int max_q, int max_k, int64_t total_q, int64_t total_k,
+                        int hq, int hkv, int d, const int64_t* strides, float scale, int causal, void* ws,
+                        size_t ws_bytes, void* stream) {
+  int rc = check_attn_common(batch, max_q, max_k, total_q, total_k, hq, hkv, d, scale, cu_q, cu_k);
+  if (rc) return rc;
+  if (strides == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "strides must not be NULL");
+  const bool nq = total_q > 0, nk = total_k > 0;
+  if ((rc = check_tensor("q", q, strides + 0, nq)) || (rc = check_tensor("k", k, strides + 2, nk)) ||
+      (rc = check_tensor("v", v, strides + 4, nk)) || (rc = check_tensor("o", o, strides + 6, nq)))
+    return rc;
+  if (nq && (lse == nullptr || (reinterpret_cast<uintptr_t>(lse) & 3u)))
+    return fail(SIQ_ERR_ALIGNMENT, "lse must be a non-NULL 4-byte aligned fp32 pointer");
+  if (batch == 0 || total_q == 0) return ok();
+  const AttnLayout L = attn_layout(batch, total_q, total_k, hq, false);
+  if (ws == nullptr || ws_bytes < L.total || !aligned16(ws))
+    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", L.total, ws_bytes);
+
+  char* base = static_cast<char*>(ws);
+  siq::AttnParams p{};
+  p.q = static_cast<const siq::bf16*>(q);
+  p.k = static_cast<const siq::bf16*>(k);
+  p.v = static_cast<const siq::bf16*>(v);
+  p.out = static_cast<siq::bf16*>(o);
+  p.lse = lse;
+  p.seq = reinterpret_cast<const siq::SeqInfo*>(base + L.seq);
+  p.qtiles = reinterpret_cast<const int2*>(base + L.qtiles);
+  p.batch = batch;
+  p.hq = hq;
+  p.hkv = hkv;
+  p.n_rep = hq / hkv;
+  p.q_tok = strides[0];
+  p.q_head = strides[1];
+  p.k_tok = strides[2];
+  p.k_head = strides[3];
+  p.v_tok = strides[4];
+  p.v_head = strides[5];
+  p.o_tok = strides[6];
+  p.o_head = strides[7];
+  p.lse_head = total_q;
+  p.total_q = total_q;
+  p.total_k = total_k;
+  p.scale = scale;
+  p.scale_log2 = scale * siq::kLog2e;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0,
+                                      reinterpret_cast<siq::SeqInfo*>(base + L.seq),
+                                      reinterpret_cast<int2*>(base + L.qtiles), L.qcap, nullptr, 0, s);
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
+  e = siq::launch_attn_fwd(p, d, causal != 0, L.qcap, s);
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "attention forward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                        const void* dout, void* dq, void* dk, void* dv, const int32_t* cu_q, const int32_t* cu_k,
+                        int batch, int max_q, int max_k, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
+                        const int64_t* strides, float scale, int causal, void* ws, size_t ws_bytes,
+                        void* stream) {
+  int rc = check_attn_common(batch, max_q, max_k, total_q, total_k, hq, hkv, d, scale, cu_q, cu_k);
+  if (rc) return rc;
+  if (strides == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "strides must not be NULL");
+  const bool nq = total_q > 0, nk = total_k > 0;
+  if ((rc = check_tensor("q", q, strides + 0, nq)) || (rc = check_tensor("k", k, strides + 2, nk)) ||
+      (rc = check_tensor("v", v, strides + 4, nk)) || (rc = check_tensor("o", o, strides + 6, nq)) ||
+      (rc = check_tensor("dout", dout, strides + 8, nq)) || (rc = check_tensor("dq", dq, strides + 10, nq)) ||
+      (rc = check_tensor("dk", dk, strides + 12, nk)) || (rc = check_tensor("dv", dv, strides + 14, nk)))
+    return rc;
+  if (nq && (lse == nullptr || (reinterpret_cast<uintptr_t>(lse) & 3u)))
+    return fail(SIQ_ERR_ALIGNMENT, "lse must be a non-NULL 4-byte aligned fp32 pointer");
+  if (batch == 0 || (total_q == 0 && total_k == 0)) return ok();
+  const AttnLayout L = attn_layout(batch, total_q, total_k, hq, true);
+  if (ws == nullptr || ws_bytes < L.total || !aligned16(ws))
+    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", L.total, ws_bytes);
+
+  char* base = static_cast<char*>(ws);
+  siq::AttnParams p{};
+  p.q = static_cast<const siq::bf16*>(q);
+  p.k = static_cast<const siq::bf16*>(k);
+  p.v = static_cast<const siq::bf16*>(v);
+  p.o = static_cast<const siq::bf16*>(o);
+  p.dout = static_cast<const siq::bf16*>(dout);
+  p.lse = const_cast<float*>(lse);
+  p.dq = static_cast<siq::bf16*>(dq);
+  p.dk = static_cast<siq::bf16*>(dk);
+  p.dv = static_cast<siq::bf16*>(dv);
+  p.delta = reinterpret_cast<float*>(base + L.delta);
+  p.seq = reinterpret_cast<const siq::SeqInfo*>(base + L.seq);
+  p.qtiles = reinterpret_cast<const int2*>(base + L.qtiles);
+  p.kvtiles = reinterpret_cast<const int2*>(base + L.kvtiles);
+  p.batch = batch;
+  p.hq = hq;
+  p.hkv = hkv;
+  p.n_rep = hq / hkv;
+  p.q_tok = strides[0];
+  p.q_head = strides[1];
+  p.k_tok = strides[2];
+  p.k_head = strides[3];
+  p.v_tok = strides[4];
+  p.v_head = strides[5];
+  p.o_tok = strides[6];
+  p.o_head = strides[7];
+  p.do_tok = strides[8];
+  p.do_head = strides[9];
+  p.dq_tok = strides[10];
+  p.dq_head = strides[11];
+  p.dk_tok = strides[12];
+  p.dk_head = strides[13];
+  p.dv_tok = strides[14];
+  p.dv_head = strides[15];
+  p.lse_head = total_q;
+  p.total_q = total_q;
+  p.total_k = total_k;
+  p.scale = scale;
+  p.scale_log2 = scale * siq::kLog2e;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0,
+                                      reinterpret_cast<siq::SeqInfo*>(base + L.seq),
+                                      reinterpret_cast<int2*>(base + L.qtiles), L.qcap,
+                                      reinterpret_cast<int2*>(base + L.kvtiles), L.kvcap, s);
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
+  e = siq::launch_attn_bwd(p, d, causal != 0, L.qcap, L.kvcap, s);
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "attention backward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+size_t siq_flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk_tokens, int need_dweight) {
+  if (n < 0 || hdim <= 0 || vocab <= 0) return 0;
+  return siq::flce_workspace_bytes(n, hdim, vocab, chunk_tokens, need_dweight != 0);
+}
+
+int siq_flce_fwd_bwd(const void* hidden, const void* weight, const int64_t* labels, int64_t n, int64_t hdim,
+                     int64_t vocab, int64_t ignore_index, int reduction, const float* divisor, float* loss,
+                     int64_t* count, int64_t* bad_labels, void* dhidden, void* dweight, int64_t chunk_tokens,
+                     void* ws, size_t ws_bytes, void* stream) {
+  if (n < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "n must be >= 0");
+  if (hdim <= 0 || vocab <= 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "hdim and vocab must be positive");
+  if (hdim % 64 != 0) return fail(SIQ_ERR_UNSUPPORTED, "hdim (%lld) must be a multiple of 64", (long long)hdim);
+  if (vocab % 8 != 0) return fail(SIQ_ERR_UNSUPPORTED, "vocab (%lld) must be a multiple of 8", (long long)vocab);
+  if (vocab >= (int64_t(1) << 31) || n >= (int64_t(1) << 31))
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "n and vocab must be < 2^31");
+  if (reduction != 0 && reduction != 1) return fail(SIQ_ERR_INVALID_ARGUMENT, "reduction must be 0 (mean) or 1 (sum/divisor)");
+  if (reduction == 1 && divisor == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "reduction 1 needs a divisor pointer");
+  if (loss == nullptr || count == nullptr || bad_labels == nullptr)
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "loss, count and bad_labels must not be NULL");
+  if (n > 0) {
+    if (hidden == nullptr || labels == nullptr || dhidden == nullptr)
+      return fail(SIQ_ERR_INVALID_ARGUMENT, "hidden, labels and dhidden must not be NULL");
+    if (!aligned16(hidden) || !aligned16(dhidden)) return fail(SIQ_ERR_ALIGNMENT, "hidden/dhidden not 16-byte aligned");
+  }
+  if (weight == nullptr || !aligned16(weight)) return fail(SIQ_ERR_ALIGNMENT, "weight must be non-NULL and 16-byte aligned");
+  if (dweight != nullptr && !aligned16(dweight)) return fail(SIQ_ERR_ALIGNMENT, "dweight not 16-byte aligned");
+  if (chunk_tokens <= 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "chunk_tokens must be positive");
+  const size_t need = siq::flce_workspace_bytes(n, hdim, vocab, chunk_tokens, dweight != nullptr);
+  if (ws == nullptr || ws_bytes < need || !aligned16(ws))
+    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
+  siq::FlceArgs a{};
+  a.hidden = static_cast<const siq::bf16*>(hidden);
+  a.weight = static_cast<const siq::bf16*>(weight);
+  a.labels = labels;
+  a.n = n;
+  a.hdim = hdim;
+  a.vocab = vocab;
+  a.ignore_index = ignore_index;
+  a.reduction = reduction;
+  a.divisor = divisor;
+  a.loss = loss;
+  a.count = count;
+  a.bad_labels = bad_labels;
+  a.dhidden = static_cast<siq::bf16*>(dhidden);
+  a.dweight = static_cast<siq::bf16*>(dweight);
+  a.chunk = chunk_tokens;
+  a.ws = ws;
+  const hipError_t e = siq::flce_run(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "fused CE launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int siq_scale_bf16_inplace(void* data, int64_t numel, const float* scalar, void* stream) {
+  if (numel < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "numel must be >= 0");
+  if (numel == 0) return ok();
+  if (data == nullptr || scalar == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "data and scalar must not be NULL");
+  if (!aligned16(data)) return fail(SIQ_ERR_ALIGNMENT, "data not 16-byte aligned");
+  const hipError_t e = siq::launch_scale_bf16(static_cast<siq::bf16*>(data), numel, scalar,
+                                              static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "scale launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+}  // extern "C"

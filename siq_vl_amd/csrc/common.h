@@ -1,0 +1,89 @@
+// Shared device helpers for the SiQ-VL hot-path kernels (gfx950 / CDNA4).
+//
+// Conventions used by every kernel in this directory:
+//  * wavefront = 64 lanes; MFMA = v_mfma_f32_32x32x16_bf16 (A 32x16, B 16x32,
+//    D 32x32 fp32).  For that instruction lane l supplies row (l % 32) of A /
+//    column (l % 32) of B and the 8 bf16 of "k-slot group" h = l / 32.  The
+//    hardware pairs A and B by (h, register) slot, so the numbering of k inside
+//    one instruction is a free choice as long as both operands use the same one.
+//  * D layout: lane l, accumulator element r (0..15) holds
+//        row = 8*(r/4) + 4*(l/32) + (r%4),  col = l % 32.
+//    Loading A-operand row m from source row perm32(m) (bits 2 and 3 swapped)
+//    turns that into  row' = 16*(r/8) + 8*(l/32) + (r%8): the 8 accumulators
+//    r = 8j..8j+7 of a lane are 8 *consecutive* source rows.  That is what lets
+//    a D tile be fed straight back as the B operand of the next MFMA (k-slot
+//    (h, i) <-> row 16j + 8h + i) and lets outputs leave as 16-byte stores.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace siq {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kWave = 64;
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// Row permutation applied to A-operand rows (see header comment).
+__device__ __forceinline__ int perm32(int m) {
+  return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1);
+}
+
+// Row (within a 32-row MFMA tile) that accumulator r of this lane refers to,
+// when the A operand was loaded through perm32.
+__device__ __forceinline__ int drow(int r, int h) { return 16 * (r >> 3) + 8 * h + (r & 7); }
+
+__device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ bf16x8 zero_bf16x8() {
+  u32x4 z = {0u, 0u, 0u, 0u};
+  return __builtin_bit_cast(bf16x8, z);
+}
+
+// Pack 8 fp32 (accumulators base..base+7 of an f32x16) into bf16 (RNE).
+__device__ __forceinline__ bf16x8 pack8(const f32x16& v, int base) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (bf16)v[base + i];
+  return r;
+}
+
+__device__ __forceinline__ bf16x8 ld_bf16x8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+__device__ __forceinline__ void st_bf16x8(bf16* p, const bf16x8& v) { *reinterpret_cast<bf16x8*>(p) = v; }
+
+// 4 rows x 8 bf16 (each row a u32x4) -> 8 columns x 4 bf16 (u32x2 each):
+// out[j] = {r0[j], r1[j], r2[j], r3[j]}.
+__device__ __forceinline__ void transpose4x8(const u32x4 (&rows)[4], u32x2 (&cols)[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t a0 = rows[0][w], a1 = rows[1][w], a2 = rows[2][w], a3 = rows[3][w];
+    cols[2 * w][0] = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
+    cols[2 * w][1] = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
+    cols[2 * w + 1][0] = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
+    cols[2 * w + 1][1] = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
+  }
+}
+
+__device__ __forceinline__ float wave_max_xor32(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+__device__ __forceinline__ float wave_sum_xor32(float x) { return x + __shfl_xor(x, 32); }
+
+}  // namespace siq

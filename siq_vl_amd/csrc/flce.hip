@@ -1,0 +1,691 @@
+// Fused lm_head linear + cross-entropy (forward and backward) for gfx950.
+//
+// Semantics: the reference computes logits = h W^T (transformers
+// models/qwen2/modeling_qwen2.py:465), upcasts them to fp32 and calls
+// F.cross_entropy(ignore_index=-100) with "mean" over non-ignored rows, or
+// "sum" divided by num_items_in_batch (loss/loss_utils.py:32-71).  Here:
+//   loss = sum_valid (lse_n - z_{n,y_n}) * inv_den,
+//   dZ   = (softmax(z_n) - onehot(y_n)) * inv_den  (0 for ignored rows),
+//   dH = dZ W,  dW = dZ^T H.
+//
+// Pipeline per chunk of C token rows (the only logits-sized buffer is one
+// chunk's softmax numerators):
+//  1. logits GEMM  Z^T = W H_c^T (MFMA, 256x256 tiles, K = hdim).  The epilogue
+//     never writes z: per (token, 256-column vocab tile) it keeps the tile
+//     max m and the sum s of exp(z - m) (the chunked-vocab logsumexp), the
+//     label logit z_y, and E = exp(z - m) in bf16 (a value in (0, 1], so bf16
+//     keeps full relative precision however large the logits are).
+//  2. row reduce: lse = M + log(sum_t s_t exp(m_t - M)); per tile the factor
+//     f = exp(m_t - lse) * g (g = inv_den or 0), so that dZ = E * f - g * [v == y].
+//  3. dH GEMM  dH_c^T = W^T dZ_c^T (split over the vocab) and
+//  4. dW GEMM  dW^T = H_c^T dZ_c, both forming dZ from E on the fly while
+//     staging it into LDS (one multiply per element; no exp in the GEMMs).
+// With several chunks dW accumulates in an fp32 workspace.  Every reduction
+// has a fixed order, so results are bitwise reproducible.
+#include "flce.h"
+
+namespace siq {
+
+namespace {
+
+constexpr int BI = 256, BJ = 256, BK = 32, NT = 256;
+constexpr int LS = BK + 8;          // LDS row stride of a staged [256][32] operand tile
+constexpr int TILE_EL = 256 * LS;   // bf16 elements per staged operand
+constexpr int kVT = BI;             // vocab columns per logits tile
+constexpr int kXcds = 8;
+
+struct GOp {
+  const bf16* base;
+  int64_t ld, rows, cols;  // element (r, c) at base[r * ld + c]; 16-byte chunks along c
+};
+
+// One 4-row x 8-column unit (global layout) per thread, staged into a
+// k-contiguous [256][32] LDS tile.  KC: the tile's k runs along the global
+// column (row-major store); otherwise along the global row (transposed store).
+template <bool KC>
+struct Stage {
+  u32x4 v[4];
+  int c, g;
+  int64_t grow, gcol;  // global origin of this thread's unit
+  __device__ __forceinline__ void init(int tid) {
+    if (KC) {
+      c = tid % (BK / 8);
+      g = tid / (BK / 8);
+    } else {
+      g = tid % (BK / 4);
+      c = tid / (BK / 4);
+    }
+  }
+  __device__ __forceinline__ void load(const GOp& op, int64_t r0, int64_t k0) {
+    if (KC) {
+      grow = r0 + 4 * g;
+      gcol = k0 + 8 * c;
+    } else {
+      grow = k0 + 4 * g;
+      gcol = r0 + 8 * c;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool ok = (grow + j < op.rows) && (gcol < op.cols);
+      v[j] = ok ? *reinterpret_cast<const u32x4*>(op.base + (grow + j) * op.ld + gcol) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  __device__ __forceinline__ void store(bf16* s) const {
+    if (KC) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(s + (4 * g + j) * LS + 8 * c) = v[j];
+    } else {
+      u32x2 cols[8];
+      transpose4x8(v, cols);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x2*>(s + (8 * c + j) * LS + 4 * g) = cols[j];
+    }
+  }
+};
+
+// dZ from E on the fly: rows = chunk tokens, cols = vocab.
+struct DzForm {
+  const float* f;        // [C, nvt]
+  const float* g;        // [C]
+  const int64_t* y;      // [C] labels of the chunk
+  int64_t nvt, nc, vocab;
+  __device__ __forceinline__ void apply(u32x4 (&v)[4], int64_t tok0, int64_t v0) const {
+    if (v0 >= vocab) return;  // zero-filled padding columns: no factor to apply
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = tok0 + j;
+      if (t >= nc) continue;
+      const float fv = f[t * nvt + v0 / kVT];
+      const float gv = g[t];
+      const int64_t yv = y[t];
+      bf16x8 e = __builtin_bit_cast(bf16x8, v[j]);
+      bf16x8 o;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float d = (float)e[i] * fv;
+        if (v0 + i == yv) d -= gv;
+        o[i] = (bf16)d;
+      }
+      v[j] = __builtin_bit_cast(u32x4, o);
+    }
+  }
+};
+
+// Maps a 1-D block id onto (I tile, J tile) so that the blocks sharing the
+// big operand tile run back to back on one XCD (block b is dispatched to XCD
+// b % 8): each XCD gets a contiguous run of the linear tile order, whose
+// fastest dimension is J when JFAST, I otherwise.
+template <bool JFAST>
+__device__ __forceinline__ bool tile_of(int nI, int nJ, int& ti, int& tj) {
+  const int total = nI * nJ;
+  const int per = (total + kXcds - 1) / kXcds;
+  const int lin = (int)(blockIdx.x % kXcds) * per + (int)(blockIdx.x / kXcds);
+  if (lin >= total) return false;
+  if (JFAST) {
+    ti = lin / nJ;
+    tj = lin % nJ;
+  } else {
+    tj = lin / nI;
+    ti = lin % nI;
+  }
+  return true;
+}
+
+// C[i][j] = sum_k A[i][k] B[j][k] over k in [kb, ke) with 4 waves of
+// 128x128 (4x4 MFMA 32x32 tiles).  acc[ti][tj][r] holds
+// i = i0 + 128*wi + 32*ti + drow(r, h), j = j0 + 128*wj + 32*tj + l32.
+template <bool AKC, bool BKC, bool BFORM>
+__device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B, const DzForm& form, int64_t i0,
+                                          int64_t j0, int64_t kb, int64_t ke, f32x16 (&acc)[4][4]) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int wi = w & 1, wj = w >> 1;
+  Stage<AKC> sa;
+  Stage<BKC> sb;
+  sa.init(tid);
+  sb.init(tid);
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = zero16();
+  const int nk = ke > kb ? (int)((ke - kb + BK - 1) / BK) : 0;
+  auto fetch = [&](int it) {
+    const int64_t k0 = kb + (int64_t)it * BK;
+    sa.load(A, i0, k0);
+    sb.load(B, j0, k0);
+    if (BFORM) {
+      if (BKC) form.apply(sb.v, sb.grow, sb.gcol);
+      else form.apply(sb.v, sb.grow, sb.gcol);
+    }
+  };
+  if (nk > 0) {
+    fetch(0);
+    sa.store(smem);
+    sb.store(smem + TILE_EL);
+  }
+  __syncthreads();
+  for (int it = 0; it < nk; ++it) {
+    const bf16* As = smem + (it & 1) * 2 * TILE_EL;
+    const bf16* Bs = As + TILE_EL;
+    const bool more = it + 1 < nk;
+    if (more) fetch(it + 1);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8 af[4], bfr[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        af[t] = ld_bf16x8(As + (128 * wi + 32 * t + perm32(l32)) * LS + 16 * ks + 8 * h);
+        bfr[t] = ld_bf16x8(Bs + (128 * wj + 32 * t + l32) * LS + 16 * ks + 8 * h);
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = mfma32(af[a], bfr[b], acc[a][b]);
+    }
+    if (more) {
+      bf16* nx = smem + ((it + 1) & 1) * 2 * TILE_EL;
+      sa.store(nx);
+      sb.store(nx + TILE_EL);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- logits
+struct LogitsArgs {
+  GOp W, H;               // W [V, hdim], H = hidden rows of the chunk [nc, hdim]
+  const int64_t* y;       // chunk labels
+  bf16* E;                // [nc, V]
+  float* mpart;           // [nc, nvt] tile max (log2 units)
+  float* spart;           // [nc, nvt] tile sum of exp2(z2 - m)
+  float* zy;              // [nc] label logit (natural units)
+  int64_t V, nc, nvt;
+  int nI, nJ;
+};
+
+__global__ __launch_bounds__(256) void flce_logits_kernel(const LogitsArgs p) {
+  __shared__ __align__(16) bf16 smem[4 * TILE_EL];
+  int ti, tj;
+  if (!tile_of<true>(p.nI, p.nJ, ti, tj)) return;
+  const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
+  f32x16 acc[4][4];
+  DzForm none{};
+  gemm_core<true, true, false>(smem, p.W, p.H, none, i0, j0, 0, p.W.cols, acc);
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int wi = w & 1, wj = w >> 1;
+  float* red = reinterpret_cast<float*>(smem);  // [2][256]
+  float mt[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t v = i0 + 128 * wi + 32 * a + drow(r, h);
+        const float z2 = v < p.V ? acc[a][b][r] * kLog2e : -INFINITY;
+        acc[a][b][r] = z2;
+        mx = fmaxf(mx, z2);
+      }
+    mx = wave_max_xor32(mx);
+    if (h == 0) red[wi * 256 + 128 * wj + 32 * b + l32] = mx;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int col = 128 * wj + 32 * b + l32;
+    mt[b] = fmaxf(red[col], red[256 + col]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int col = 128 * wj + 32 * b + l32;
+    const int64_t tok = j0 + col;
+    const bool tv = tok < p.nc;
+    const int64_t yv = tv ? p.y[tok] : -1;
+    float s = 0.f;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int64_t v0 = i0 + 128 * wi + 32 * a + 16 * jj + 8 * h;
+        bf16x8 e8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float z2 = acc[a][b][8 * jj + i];
+          const float e = exp2f_fast(z2 - mt[b]);
+          s += e;
+          e8[i] = (bf16)e;
+          if (v0 + i == yv) p.zy[tok] = z2 * kLn2;
+        }
+        if (tv && v0 < p.V) st_bf16x8(p.E + tok * p.V + v0, e8);
+      }
+    }
+    s = wave_sum_xor32(s);
+    if (h == 0) red[wi * 256 + col] = s;
+  }
+  __syncthreads();
+  if (wi == 0 && h == 0) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int col = 128 * wj + 32 * b + l32;
+      const int64_t tok = j0 + col;
+      if (tok < p.nc) {
+        p.mpart[tok * p.nvt + ti] = mt[b];
+        p.spart[tok * p.nvt + ti] = red[col] + red[256 + col];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- row reduce
+struct ReduceArgs {
+  float* mpart;  // in: tile max; out: f = exp2(m - lse2) * g
+  const float* spart;
+  const float* zy;
+  const int64_t* y;      // chunk labels
+  float* g;              // [nc]
+  float* loss_row;       // [nc] (chunk slice)
+  const float* invden;
+  int64_t nc, nvt, V, ignore_index;
+};
+
+__global__ __launch_bounds__(256) void flce_reduce_kernel(const ReduceArgs p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.nc) return;
+  float* m = p.mpart + row * p.nvt;
+  const float* s = p.spart + row * p.nvt;
+  float mx = -INFINITY;
+  for (int64_t t = lane; t < p.nvt; t += 64) mx = fmaxf(mx, m[t]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  float sum = 0.f;
+  for (int64_t t = lane; t < p.nvt; t += 64) sum += s[t] * exp2f_fast(m[t] - mx);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+  const float lse2 = mx + __log2f(sum);
+  const int64_t yv = p.y[row];
+  const bool valid = yv != p.ignore_index && yv >= 0 && yv < p.V;
+  const float gv = valid ? *p.invden : 0.f;
+  for (int64_t t = lane; t < p.nvt; t += 64) m[t] = exp2f_fast(m[t] - lse2) * gv;
+  if (lane == 0) {
+    p.g[row] = gv;
+    p.loss_row[row] = valid ? lse2 * kLn2 - p.zy[row] : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------- dH
+struct DhArgs {
+  GOp Wt;        // W [V, hdim] read as A[i = h][k = v]
+  GOp E;         // [nc, V] read as B[j = tok][k = v]
+  DzForm form;
+  bf16* dh;      // dhidden rows of the chunk [nc, hdim] (used when splits == 1)
+  float* part;   // [splits, nc, hdim]
+  int64_t hdim, nc, kper;
+  int nI, nJ, splits;
+};
+
+__global__ __launch_bounds__(256) void flce_dh_kernel(const DhArgs p) {
+  __shared__ __align__(16) bf16 smem[4 * TILE_EL];
+  int ti, tj;
+  if (!tile_of<false>(p.nI, p.nJ, ti, tj)) return;
+  const int split = blockIdx.y;
+  const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
+  const int64_t kb = split * p.kper;
+  const int64_t ke = min(p.E.cols, kb + p.kper);
+  f32x16 acc[4][4];
+  gemm_core<false, true, true>(smem, p.Wt, p.E, p.form, i0, j0, kb, ke, acc);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int wi = w & 1, wj = w >> 1;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int64_t tok = j0 + 128 * wj + 32 * b + l32;
+    if (tok >= p.nc) continue;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int64_t hh = i0 + 128 * wi + 32 * a + 16 * jj + 8 * h;
+        if (hh >= p.hdim) continue;
+        if (p.splits == 1) {
+          bf16x8 o;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = (bf16)acc[a][b][8 * jj + i];
+          st_bf16x8(p.dh + tok * p.hdim + hh, o);
+        } else {
+          float* dst = p.part + ((int64_t)split * p.nc + tok) * p.hdim + hh;
+          f32x4 lo, hi;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            lo[i] = acc[a][b][8 * jj + i];
+            hi[i] = acc[a][b][8 * jj + 4 + i];
+          }
+          *reinterpret_cast<f32x4*>(dst) = lo;
+          *reinterpret_cast<f32x4*>(dst + 4) = hi;
+        }
+      }
+  }
+}
+
+__global__ __launch_bounds__(256) void flce_dh_sum_kernel(const float* __restrict__ part, bf16* __restrict__ dh,
+                                                          int64_t nvec, int64_t stride, int splits) {
+  // nvec groups of 8 elements; part is [splits][stride] with stride = nc * hdim.
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += (int64_t)gridDim.x * 256) {
+    f32x4 a = *reinterpret_cast<const f32x4*>(part + 8 * i);
+    f32x4 b = *reinterpret_cast<const f32x4*>(part + 8 * i + 4);
+    for (int s = 1; s < splits; ++s) {
+      a += *reinterpret_cast<const f32x4*>(part + s * stride + 8 * i);
+      b += *reinterpret_cast<const f32x4*>(part + s * stride + 8 * i + 4);
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[k] = (bf16)a[k];
+      o[4 + k] = (bf16)b[k];
+    }
+    st_bf16x8(dh + 8 * i, o);
+  }
+}
+
+// ---------------------------------------------------------------- dW
+struct DwArgs {
+  GOp Ht;        // hidden rows of the chunk [nc, hdim] read as A[i = h][k = tok]
+  GOp Et;        // [nc, V] read as B[j = v][k = tok]
+  DzForm form;
+  bf16* dw;      // [V, hdim]
+  float* acc32;  // [V, hdim] fp32 accumulator across chunks
+  int64_t hdim, V;
+  int nI, nJ;
+  int mode;      // 0: bf16 store; 1: fp32 store; 2: fp32 add; 3: fp32 add + bf16 store
+};
+
+__global__ __launch_bounds__(256) void flce_dw_kernel(const DwArgs p) {
+  __shared__ __align__(16) bf16 smem[4 * TILE_EL];
+  int ti, tj;
+  if (!tile_of<false>(p.nI, p.nJ, ti, tj)) return;
+  const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
+  f32x16 acc[4][4];
+  gemm_core<false, false, true>(smem, p.Ht, p.Et, p.form, i0, j0, 0, p.Ht.rows, acc);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int wi = w & 1, wj = w >> 1;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int64_t v = j0 + 128 * wj + 32 * b + l32;
+    if (v >= p.V) continue;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int64_t hh = i0 + 128 * wi + 32 * a + 16 * jj + 8 * h;
+        if (hh >= p.hdim) continue;
+        f32x4 lo, hi;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lo[i] = acc[a][b][8 * jj + i];
+          hi[i] = acc[a][b][8 * jj + 4 + i];
+        }
+        float* a32 = p.acc32 + v * p.hdim + hh;
+        if (p.mode >= 2) {
+          lo += *reinterpret_cast<const f32x4*>(a32);
+          hi += *reinterpret_cast<const f32x4*>(a32 + 4);
+        }
+        if (p.mode == 1 || p.mode == 2) {
+          *reinterpret_cast<f32x4*>(a32) = lo;
+          *reinterpret_cast<f32x4*>(a32 + 4) = hi;
+        } else {
+          bf16x8 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            o[i] = (bf16)lo[i];
+            o[4 + i] = (bf16)hi[i];
+          }
+          st_bf16x8(p.dw + v * p.hdim + hh, o);
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------- scalars
+__global__ __launch_bounds__(1024) void flce_count_kernel(const int64_t* __restrict__ y, int64_t n, int64_t V,
+                                                          int64_t ignore_index, int reduction,
+                                                          const float* __restrict__ divisor, int64_t* count,
+                                                          int64_t* bad, float* invden) {
+  __shared__ long long sc[1024], sb[1024];
+  long long c = 0, b = 0;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) {
+    const int64_t v = y[i];
+    if (v == ignore_index) continue;
+    if (v >= 0 && v < V) ++c;
+    else ++b;
+  }
+  sc[threadIdx.x] = c;
+  sb[threadIdx.x] = b;
+  __syncthreads();
+  for (int s = 512; s >= 1; s >>= 1) {
+    if ((int)threadIdx.x < s) {
+      sc[threadIdx.x] += sc[threadIdx.x + s];
+      sb[threadIdx.x] += sb[threadIdx.x + s];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    *count = sc[0];
+    *bad = sb[0];
+    *invden = reduction == 0 ? 1.f / (float)sc[0] : 1.f / *divisor;
+  }
+}
+
+__global__ __launch_bounds__(1024) void flce_loss_kernel(const float* __restrict__ loss_row, int64_t n,
+                                                         const float* __restrict__ invden, float* loss) {
+  __shared__ float sm[1024];
+  float acc = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) acc += loss_row[i];
+  sm[threadIdx.x] = acc;
+  __syncthreads();
+  for (int s = 512; s >= 1; s >>= 1) {
+    if ((int)threadIdx.x < s) sm[threadIdx.x] += sm[threadIdx.x + s];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *loss = sm[0] * *invden;
+}
+
+__global__ __launch_bounds__(256) void scale_bf16_kernel(bf16* __restrict__ x, int64_t nvec, int64_t numel,
+                                                         const float* __restrict__ scalar) {
+  const float s = *scalar;
+  if (s == 1.f) return;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += (int64_t)gridDim.x * 256) {
+    if (8 * i + 8 <= numel) {
+      bf16x8 v = ld_bf16x8(x + 8 * i);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = (bf16)((float)v[k] * s);
+      st_bf16x8(x + 8 * i, v);
+    } else {
+      for (int64_t k = 8 * i; k < numel; ++k) x[k] = (bf16)((float)x[k] * s);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void zero_bf16_kernel(bf16* __restrict__ x, int64_t nvec) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += (int64_t)gridDim.x * 256)
+    *reinterpret_cast<u32x4*>(x + 8 * i) = u32x4{0u, 0u, 0u, 0u};
+}
+
+// ---------------------------------------------------------------- workspace
+struct Layout {
+  size_t invden, loss_row, g, mpart, spart, zy, E, part, acc32, total;
+  int64_t chunk, nvt, splits;
+};
+
+size_t al(size_t x) { return (x + 255) & ~size_t(255); }
+
+int dh_splits(int64_t hdim, int64_t chunk) {
+  const int64_t tiles = ((hdim + BI - 1) / BI) * ((chunk + BJ - 1) / BJ);
+  int64_t s = (1024 + tiles - 1) / tiles;
+  if (s < 1) s = 1;
+  if (s > 8) s = 8;
+  return (int)s;
+}
+
+Layout layout(int64_t n, int64_t hdim, int64_t V, int64_t chunk, bool need_dw) {
+  Layout L{};
+  L.chunk = chunk < n ? chunk : (n > 0 ? n : 1);
+  L.nvt = (V + kVT - 1) / kVT;
+  L.splits = dh_splits(hdim, L.chunk);
+  const int64_t nchunks = n > 0 ? (n + L.chunk - 1) / L.chunk : 0;
+  size_t off = 0;
+  L.invden = off;
+  off += 256;
+  L.loss_row = off;
+  off += al(sizeof(float) * (size_t)(n > 0 ? n : 1));
+  L.g = off;
+  off += al(sizeof(float) * (size_t)L.chunk);
+  L.mpart = off;
+  off += al(sizeof(float) * (size_t)(L.chunk * L.nvt));
+  L.spart = off;
+  off += al(sizeof(float) * (size_t)(L.chunk * L.nvt));
+  L.zy = off;
+  off += al(sizeof(float) * (size_t)L.chunk);
+  L.E = off;
+  off += al(sizeof(bf16) * (size_t)(L.chunk * V));
+  L.part = off;
+  if (L.splits > 1) off += al(sizeof(float) * (size_t)(L.splits * L.chunk * hdim));
+  L.acc32 = off;
+  if (need_dw && nchunks > 1) off += al(sizeof(float) * (size_t)(V * hdim));
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+
+size_t flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk, bool need_dw) {
+  if (chunk <= 0) return 0;
+  return layout(n, hdim, vocab, chunk, need_dw).total;
+}
+
+hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
+  const Layout L = layout(a.n, a.hdim, a.vocab, a.chunk, a.dweight != nullptr);
+  char* ws = static_cast<char*>(a.ws);
+  float* invden = reinterpret_cast<float*>(ws + L.invden);
+  float* loss_row = reinterpret_cast<float*>(ws + L.loss_row);
+  float* g = reinterpret_cast<float*>(ws + L.g);
+  float* mpart = reinterpret_cast<float*>(ws + L.mpart);
+  float* spart = reinterpret_cast<float*>(ws + L.spart);
+  float* zy = reinterpret_cast<float*>(ws + L.zy);
+  bf16* E = reinterpret_cast<bf16*>(ws + L.E);
+  float* part = reinterpret_cast<float*>(ws + L.part);
+  float* acc32 = reinterpret_cast<float*>(ws + L.acc32);
+  const int64_t V = a.vocab, Hd = a.hdim;
+
+  hipLaunchKernelGGL(flce_count_kernel, dim3(1), dim3(1024), 0, stream, a.labels, a.n, V, a.ignore_index,
+                     a.reduction, a.divisor, a.count, a.bad_labels, invden);
+  const int64_t nchunks = a.n > 0 ? (a.n + L.chunk - 1) / L.chunk : 0;
+  for (int64_t ci = 0; ci < nchunks; ++ci) {
+    const int64_t c0 = ci * L.chunk;
+    const int64_t nc = (a.n - c0) < L.chunk ? (a.n - c0) : L.chunk;
+    const bf16* Hc = a.hidden + c0 * Hd;
+    const int64_t* yc = a.labels + c0;
+
+    LogitsArgs lg{};
+    lg.W = GOp{a.weight, Hd, V, Hd};
+    lg.H = GOp{Hc, Hd, nc, Hd};
+    lg.y = yc;
+    lg.E = E;
+    lg.mpart = mpart;
+    lg.spart = spart;
+    lg.zy = zy;
+    lg.V = V;
+    lg.nc = nc;
+    lg.nvt = L.nvt;
+    lg.nI = (int)L.nvt;
+    lg.nJ = (int)((nc + BJ - 1) / BJ);
+    {
+      const int total = lg.nI * lg.nJ;
+      const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
+      hipLaunchKernelGGL(flce_logits_kernel, dim3(grid), dim3(NT), 0, stream, lg);
+    }
+
+    ReduceArgs rd{};
+    rd.mpart = mpart;
+    rd.spart = spart;
+    rd.zy = zy;
+    rd.y = yc;
+    rd.g = g;
+    rd.loss_row = loss_row + c0;
+    rd.invden = invden;
+    rd.nc = nc;
+    rd.nvt = L.nvt;
+    rd.V = V;
+    rd.ignore_index = a.ignore_index;
+    hipLaunchKernelGGL(flce_reduce_kernel, dim3((unsigned)((nc + 3) / 4)), dim3(256), 0, stream, rd);
+
+    DzForm form{mpart, g, yc, L.nvt, nc, V};
+
+    DhArgs dh{};
+    dh.Wt = GOp{a.weight, Hd, V, Hd};
+    dh.E = GOp{E, V, nc, V};
+    dh.form = form;
+    dh.dh = a.dhidden + c0 * Hd;
+    dh.part = part;
+    dh.hdim = Hd;
+    dh.nc = nc;
+    dh.splits = (int)L.splits;
+    {
+      const int64_t kblocks = (V + BK - 1) / BK;
+      dh.kper = ((kblocks + L.splits - 1) / L.splits) * BK;
+    }
+    dh.nI = (int)((Hd + BI - 1) / BI);
+    dh.nJ = (int)((nc + BJ - 1) / BJ);
+    {
+      const int total = dh.nI * dh.nJ;
+      const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
+      hipLaunchKernelGGL(flce_dh_kernel, dim3(grid, (unsigned)L.splits), dim3(NT), 0, stream, dh);
+    }
+    if (L.splits > 1) {
+      const int64_t nvec = nc * Hd / 8;
+      int64_t blocks = (nvec + 255) / 256;
+      if (blocks > 4096) blocks = 4096;
+      hipLaunchKernelGGL(flce_dh_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, part,
+                         a.dhidden + c0 * Hd, nvec, nc * Hd, (int)L.splits);
+    }
+
+    if (a.dweight != nullptr) {
+      DwArgs dw{};
+      dw.Ht = GOp{Hc, Hd, nc, Hd};
+      dw.Et = GOp{E, V, nc, V};
+      dw.form = form;
+      dw.dw = a.dweight;
+      dw.acc32 = acc32;
+      dw.hdim = Hd;
+      dw.V = V;
+      dw.nI = (int)((Hd + BI - 1) / BI);
+      dw.nJ = (int)L.nvt;
+      if (nchunks == 1) dw.mode = 0;
+      else if (ci == 0) dw.mode = 1;
+      else if (ci + 1 < nchunks) dw.mode = 2;
+      else dw.mode = 3;
+      const int total = dw.nI * dw.nJ;
+      const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
+      hipLaunchKernelGGL(flce_dw_kernel, dim3(grid), dim3(NT), 0, stream, dw);
+    }
+  }
+  if (a.n == 0 && a.dweight != nullptr) {
+    // no rows: d loss / d W is zero (a fill kernel, so the call stays graph-capturable)
+    const int64_t nvec = V * Hd / 8;
+    int64_t blocks = (nvec + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(zero_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a.dweight, nvec);
+  }
+  hipLaunchKernelGGL(flce_loss_kernel, dim3(1), dim3(1024), 0, stream, loss_row, a.n, invden, a.loss);
+  return hipGetLastError();
+}
+
+hipError_t launch_scale_bf16(bf16* data, int64_t numel, const float* scalar, hipStream_t stream) {
+  const int64_t nvec = (numel + 7) / 8;
+  int64_t blocks = (nvec + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(scale_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, data, nvec, numel, scalar);
+  return hipGetLastError();
+}
+
+}  // namespace siq
