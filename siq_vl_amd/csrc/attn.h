@@ -10,8 +10,8 @@ namespace siq {
 // Tile sizes shared by the scheduler and the kernels.
 constexpr int kFwdBM = 128;    // q rows per forward / dQ workgroup (4 waves x 32)
 constexpr int kFwdBN = 64;     // kv rows per inner step of the forward / dQ loop
-constexpr int kBwdBN = 128;    // kv rows per dK/dV workgroup (4 waves x 32)
-constexpr int kBwdBM = 64;     // q rows per inner step of the dK/dV loop
+constexpr int kBwdBN = 32;     // kv rows per dK/dV workgroup (shared by its 4 waves)
+constexpr int kBwdBM = 128;    // q rows per inner step of the dK/dV loop (4 waves x 32)
 constexpr int kSchedKeys = 2048;
 
 struct AttnParams {

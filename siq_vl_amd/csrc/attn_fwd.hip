@@ -12,25 +12,31 @@
 // One workgroup = 4 waves = 128 q rows of one q-head of one sequence; the
 // (sequence, q-tile) comes from the device-side schedule (heaviest first).
 // Each wave owns 32 q rows and keeps its Q fragment in registers as the B
-// operand of S^T = K Q^T (v_mfma_f32_32x32x16_bf16), so each lane ends up
-// holding 16 scores of ONE q row: the online-softmax max/sum is in-lane plus
-// one cross-half swap.  P^T then feeds O^T += V^T P^T directly from registers.
-// K (row-major) and V (transposed) tiles of 64 kv rows are double-buffered in
-// LDS; the next tile's global loads are in flight while the current one is
-// multiplied.
+// operand of S^T = K Q^T (v_mfma_f32_32x32x16_bf16), so each lane holds 16
+// scores of ONE q row: the online-softmax max is in-lane plus one cross-half
+// swap.  P^T then feeds O^T += V^T P^T straight from registers, with V^T read
+// from the row-major V tile by ds_read_b64_tr_b16 in the row order of the
+// score accumulators (no shuffles).  K and V tiles of 64 kv
+// rows are double-buffered in LDS; the next tile's global loads are in flight
+// while the current one is multiplied.
+//
+// Rescaling is lazy: a row's reference max only moves when a block's max
+// exceeds it by more than 2^8 (so unnormalised P stays <= 256, exact in the
+// fp32 accumulators and in bf16), and the O rescale is skipped for the whole
+// wave when no row moved -- after the first block it practically never runs.
 #include "attn.h"
 
 namespace siq {
 
 namespace {
 
+constexpr float kRescaleLog2 = 8.f;
+
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnParams p) {
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   constexpr int BM = kFwdBM, BN = kFwdBN, NT = 256;
-  using KTile = Tile4x8<BN, D, NT, false>;
-  using VTile = Tile4x8<BN, D, NT, true>;
-  constexpr int KS = KTile::RS, VS = VTile::TS;
-  constexpr int KSZ = BN * KS, VSZ = D * VS, STAGE = KSZ + VSZ;
+  using Tile = RowTile<BN, D, NT>;
+  constexpr int RS = Tile::RS, TSZ = BN * RS, STAGE = 2 * TSZ;
   __shared__ __align__(16) bf16 smem[2 * STAGE];
 
   const int2 tl = p.qtiles[blockIdx.x];
@@ -46,39 +52,47 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnParams p) {
 
   const int qrow = q0 + 32 * w + l32;
   const bool qvalid = qrow < si.q_len;
+  // last kv row this lane's q row may see
+  const int lim = CAUSAL ? min(si.k_len - 1, qrow + off) : si.k_len - 1;
   bf16x8 qf[D / 16];
   {
     const bf16* qp = p.q + (int64_t)(si.q_start + (qvalid ? qrow : 0)) * p.q_tok + (int64_t)hqi * p.q_head + 8 * h;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) qf[ks] = qvalid ? ld_bf16x8(qp + 16 * ks) : zero_bf16x8();
+    for (int ks = 0; ks < D / 16; ++ks) {
+      const bf16x8 x = ld_bf16x8(qp + 16 * ks);
+      qf[ks] = qvalid ? x : zero_bf16x8();
+    }
   }
   f32x16 oacc[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) oacc[i] = zero16();
-  float mrow = -INFINITY, lsum = 0.f;  // running max in log2 units, per-half partial sum
+  float mref = -INFINITY, lsum = 0.f;  // reference max (log2 units), per-half partial row sum
   const float c = p.scale_log2;
 
   const bf16* kbase = p.k + (int64_t)si.k_start * p.k_tok + (int64_t)hk * p.k_head;
   const bf16* vbase = p.v + (int64_t)si.k_start * p.v_tok + (int64_t)hk * p.v_head;
-  KTile kt;
-  VTile vt;
+  Tile kt, vt;
+  kt.init(p.k_tok, tid);
+  vt.init(p.v_tok, tid);
+  TrRead tr;
+  tr.init(RS, lane);
   if (nblk > 0) {
-    kt.load(kbase, p.k_tok, si.k_len, tid);
-    vt.load(vbase, p.v_tok, si.k_len, tid);
-    kt.store_rows(smem, tid);
-    vt.store_cols(smem + KSZ, tid);
+    kt.load(kbase, p.k_tok, si.k_len);
+    vt.load(vbase, p.v_tok, si.k_len);
+    kt.store(smem, tid);
+    vt.store(smem + TSZ, tid);
   }
   __syncthreads();
 
   const int wq_last = q0 + 32 * w + 31;  // last q row of this wave
   for (int kb = 0; kb < nblk; ++kb) {
     const bf16* Ks = smem + (kb & 1) * STAGE;
-    const bf16* Vt = Ks + KSZ;
+    const bf16* Vs = Ks + TSZ;
     const int k0 = kb * BN;
     const bool more = kb + 1 < nblk;
     if (more) {
-      kt.load(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN, tid);
-      vt.load(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN, tid);
+      kt.load(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN);
+      vt.load(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN);
     }
     const bool active = !CAUSAL || (k0 <= wq_last + off);
     if (active) {
@@ -86,61 +100,59 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnParams p) {
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t) {
         s[t] = zero16();
-        const bf16* kr = Ks + (32 * t + perm32(l32)) * KS + 8 * h;
+        const bf16* kr = Ks + (32 * t + l32) * RS + 8 * h;
 #pragma unroll
         for (int ks = 0; ks < D / 16; ++ks) s[t] = mfma32(ld_bf16x8(kr + 16 * ks), qf[ks], s[t]);
       }
+      // accumulator (t, r) holds kv = k0 + 32t + nrow(r, h)
       const bool need_mask = (k0 + BN > si.k_len) || (CAUSAL && k0 + BN - 1 > q0 + 32 * w + off);
+      if (need_mask) {
+        const int rel = lim - k0 - 4 * h;
+#pragma unroll
+        for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[t][r] = (32 * t + 8 * (r >> 2) + (r & 3) > rel) ? -INFINITY : s[t][r];
+      }
       float mx = -INFINITY;
 #pragma unroll
-      for (int t = 0; t < BN / 32; ++t) {
+      for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = s[t][r] * c;
-          if (need_mask) {
-            const int kv = k0 + 32 * t + drow(r, h);
-            if (kv >= si.k_len || (CAUSAL && kv > qrow + off)) x = -INFINITY;
-          }
-          s[t][r] = x;
-          mx = fmaxf(mx, x);
-        }
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+      mx = wave_max_xor32(mx) * c;
+      const bool grow = mx > mref + kRescaleLog2;
+      if (__any(grow)) {
+        // rows that did not grow keep alpha = 1 (also when their max is still -inf)
+        const float alpha = grow ? exp2f_fast(mref - mx) : 1.f;
+        mref = grow ? mx : mref;
+        lsum *= alpha;
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i) oacc[i] *= alpha;
       }
-      mx = wave_max_xor32(mx);
-      const float mnew = fmaxf(mrow, mx);
-      const float msafe = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = exp2f_fast(mrow - msafe);
-      mrow = mnew;
-      lsum *= alpha;
-#pragma unroll
-      for (int i = 0; i < D / 32; ++i) oacc[i] *= alpha;
+      const float msafe = mref == -INFINITY ? 0.f : mref;
       float ps = 0.f;
-#pragma unroll
-      for (int t = 0; t < BN / 32; ++t) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e = exp2f_fast(s[t][r] - msafe);
-          s[t][r] = e;
-          ps += e;
-        }
-      }
-      lsum += ps;
       bf16x8 pb[BN / 16];
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = exp2f_fast(__builtin_fmaf(s[t][r], c, -msafe));
+          s[t][r] = e;
+          ps += e;
+        }
         pb[2 * t] = pack8(s[t], 0);
         pb[2 * t + 1] = pack8(s[t], 8);
       }
+      lsum += ps;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt) {
-        const bf16* vr = Vt + (32 * dt + perm32(l32)) * VS + 8 * h;
 #pragma unroll
-        for (int st = 0; st < BN / 16; ++st) oacc[dt] = mfma32(ld_bf16x8(vr + 16 * st), pb[st], oacc[dt]);
+        for (int st = 0; st < BN / 16; ++st) oacc[dt] = mfma32(tr.read(Vs, RS, 16 * st, 32 * dt), pb[st], oacc[dt]);
       }
     }
     if (more) {
       bf16* nx = smem + ((kb + 1) & 1) * STAGE;
-      kt.store_rows(nx, tid);
-      vt.store_cols(nx + KSZ, tid);
+      kt.store(nx, tid);
+      vt.store(nx + TSZ, tid);
     }
     __syncthreads();
   }
@@ -161,7 +173,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnParams p) {
     }
     if (h == 0) {
       p.lse[(int64_t)hqi * p.lse_head + si.q_start + qrow] =
-          ltot > 0.f ? (mrow + __log2f(ltot)) * kLn2 : -INFINITY;
+          ltot > 0.f ? (mref + __log2f(ltot)) * kLn2 : -INFINITY;
     }
   }
 }
