@@ -40,9 +40,18 @@ def sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
+# MFMA results in VGPRs instead of AGPRs for the attention kernels: their
+# score / dP accumulators feed VALU softmax code every step, and the AGPR form
+# made the register allocator shuttle values between the two files.
+PER_FILE_FLAGS = {
+    "attn_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "attn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = OBJ_DIR / (src.name + ".o")
-    cmd = [_hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, *PER_FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")

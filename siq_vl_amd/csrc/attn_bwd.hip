@@ -13,8 +13,8 @@
 //    sit in every wave's registers as B operands of S = Q K^T and dP = dO V^T
 //    (lane = kv column).  The workgroup walks every q-head of the GQA group and
 //    every q block that can see the rows, 128 q rows per step (32 per wave),
-//    with Q and dO tiles staged row-major in LDS; dV^T += dO^T P and
-//    dK^T += Q^T dS read dO^T / Q^T with ds_read_b64_tr_b16.  The four waves'
+//    with Q and dO tiles staged in LDS by direct global->LDS loads; dV^T +=
+//    dO^T P and dK^T += Q^T dS read dO^T / Q^T with ds_read_b64_tr_b16.  The four waves'
 //    partial dK/dV are summed through LDS at the end and written once.
 //  * dQ: one workgroup = 128 q rows of one q-head (same schedule as the
 //    forward); Q and dO in registers as B operands of S^T = K Q^T and
@@ -50,20 +50,29 @@ template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnParams p) {
   constexpr int BN = kBwdBN, BM = kBwdBM, NT = 256;
   static_assert(BN == 32 && BM == 128, "one 32-row kv tile, 32 q rows per wave");
-  using QTile = RowTile<BM, D, NT>;
-  constexpr int RS = QTile::RS, TSZ = BM * RS;
-  constexpr int STAGE = 2 * TSZ;  // Q, dO (bf16 elements)
+  using QTile = LdsTile<BM, D, NT / 64>;
+  constexpr int TE = QTile::ELEMS;
+  constexpr int STAGE = 2 * TE;  // Q, dO (bf16 elements)
   __shared__ __align__(16) bf16 smem[2 * STAGE];
-  __shared__ __align__(16) float rowv[2][2][BM];  // [stage][lse2 | delta][q]
+  __shared__ __align__(16) float rowv[2][2][BM];  // [stage][lse | delta][q] (raw, as loaded)
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int wu = wave_uniform(w);
+  QTile qt, gt;
+  qt.init(p.q_tok, lane);
+  gt.init(p.do_tok, lane);
+  RowRead<D> rr;
+  rr.init(lane);
+  TrRead<D> tr;
+  tr.init(lane);
+  const float c = p.scale_log2;
 
   const int2 tl = p.kvtiles[blockIdx.x];
   if (tl.x < 0) return;
   const SeqInfo si = p.seq[tl.x];
   const int hk = blockIdx.y;
   const int k0 = tl.y * BN;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int off = si.k_len - si.q_len;
-  const float c = p.scale_log2;
 
   const int kvrow = k0 + l32;
   const bool kvvalid = kvrow < si.k_len;
@@ -92,53 +101,39 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnParams p) 
   const int nqb = si.q_len > qb0 * BM ? (si.q_len - qb0 * BM + BM - 1) / BM : 0;
   const int nsteps = (k0 < si.k_len) ? nqb * p.n_rep : 0;
 
-  QTile qt, gt;
-  qt.init(p.q_tok, tid);
-  gt.init(p.do_tok, tid);
-  TrRead tr;
-  tr.init(RS, lane);
-  float rl = 0.f, rd = 0.f;  // this thread's lse2 / delta prefetch (threads < BM)
-  auto fetch = [&](int step) {
+  // Stage step `step` into buffer `buf`: Q and dO tiles, plus the 128 LSE and
+  // Delta values (one 64-lane dword direct load per wave; rows past the end
+  // read the last valid row and are fixed at use).
+  auto issue = [&](int step, int buf) {
     const int j = step / nqb, qb = qb0 + step - j * nqb;
     const int hq = hk * p.n_rep + j;
     const int q0 = qb * BM;
     const int nrows = si.q_len - q0;
     const int64_t r0 = si.q_start + q0;
-    qt.load(p.q + r0 * p.q_tok + (int64_t)hq * p.q_head, p.q_tok, nrows);
-    gt.load(p.dout + r0 * p.do_tok + (int64_t)hq * p.do_head, p.do_tok, nrows);
-    if (tid < BM) {
-      const bool ok = tid < nrows;
-      const int64_t idx = (int64_t)hq * p.lse_head + r0 + (ok ? tid : 0);
-      const float l = p.lse[idx], dl = p.delta[idx];
-      rl = ok ? l * kLog2e : INFINITY;  // invalid rows: P = exp2(-inf) = 0
-      rd = ok ? dl : 0.f;
-    }
-  };
-  auto stash = [&](int buf) {
     bf16* base = smem + buf * STAGE;
-    qt.store(base, tid);
-    gt.store(base + TSZ, tid);
-    if (tid < BM) {
-      rowv[buf][0][tid] = rl;
-      rowv[buf][1][tid] = rd;
-    }
+    qt.issue(p.q + r0 * p.q_tok + (int64_t)hq * p.q_head, p.q_tok, nrows, base, wu);
+    gt.issue(p.dout + r0 * p.do_tok + (int64_t)hq * p.do_head, p.do_tok, nrows, base + TE, wu);
+    const int which = wu >> 1, half = wu & 1;
+    const int r = min(64 * half + lane, nrows - 1);
+    const float* src = (which == 0 ? p.lse : p.delta) + (int64_t)hq * p.lse_head + r0 + r;
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)(&rowv[buf][which][64 * half]), 4, 0, 0);
   };
 
-  if (nsteps > 0) {
-    fetch(0);
-    stash(0);
-  }
+  if (nsteps > 0) issue(0, 0);
+  wait_vmem();
   __syncthreads();
 
   for (int step = 0; step < nsteps; ++step) {
     const int buf = step & 1;
     const bf16* Qs = smem + buf * STAGE;
-    const bf16* Gs = Qs + TSZ;
-    const float* lse2 = rowv[buf][0];
+    const bf16* Gs = Qs + TE;
+    const float* lse = rowv[buf][0];
     const float* dlt = rowv[buf][1];
     const int q0 = (qb0 + step % nqb) * BM;
+    const int qvalid = si.q_len - q0;  // rows of this block that exist
+    const bool tail = qvalid < BM;
     const bool more = step + 1 < nsteps;
-    if (more) fetch(step + 1);
+    if (more) issue(step + 1, buf ^ 1);
 
     const int wq0 = q0 + 32 * w;  // first q row of this wave
     const bool active = !CAUSAL || (wq0 + 31 + off >= k0);
@@ -146,26 +141,29 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnParams p) 
       const bool need_mask = CAUSAL && (wq0 + off < k0 + 31);
       // accumulator r (= 8j + i) holds q = wq0 + 16j + krow(i, h), kv = kvrow
       f32x16 s = zero16(), dp = zero16();
-      const bf16* qr = Qs + (32 * w + l32) * RS + 8 * h;
-      const bf16* gr = Gs + (32 * w + l32) * RS + 8 * h;
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
-        s = mfma32(ld_bf16x8(qr + 16 * ks), kf[ks], s);
-        dp = mfma32(ld_bf16x8(gr + 16 * ks), vf[ks], dp);
+        s = mfma32(rr.read(Qs, 32 * w, ks), kf[ks], s);
+        dp = mfma32(rr.read(Gs, 32 * w, ks), vf[ks], dp);
       }
       const int rel = kvrow - off - wq0 - 4 * h;  // causal: keep q offsets >= rel
       bf16x8 pb[2], db[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int qo = 32 * w + 16 * j + 4 * h;  // krow(i, h) = 4h + i (i < 4), 8 + 4h + i - 4
-        const f32x4 l0 = *reinterpret_cast<const f32x4*>(lse2 + qo);
-        const f32x4 l1 = *reinterpret_cast<const f32x4*>(lse2 + qo + 8);
+        const f32x4 l0 = *reinterpret_cast<const f32x4*>(lse + qo);
+        const f32x4 l1 = *reinterpret_cast<const f32x4*>(lse + qo + 8);
         const f32x4 d0 = *reinterpret_cast<const f32x4*>(dlt + qo);
         const f32x4 d1 = *reinterpret_cast<const f32x4*>(dlt + qo + 8);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float lv = i < 4 ? l0[i] : l1[i - 4];
-          const float dv_ = i < 4 ? d0[i] : d1[i - 4];
+          float lv = (i < 4 ? l0[i] : l1[i - 4]) * kLog2e;
+          float dv_ = i < 4 ? d0[i] : d1[i - 4];
+          if (tail) {  // rows past the end of the sequence: P = exp2(-inf) = 0, Delta = 0
+            const bool ok = qo + 8 * (i >> 2) + (i & 3) < qvalid;
+            lv = ok ? lv : INFINITY;
+            dv_ = ok ? dv_ : 0.f;
+          }
           float pv = exp2f_fast(__builtin_fmaf(s[8 * j + i], c, -lv));
           if (need_mask) pv = (16 * j + 8 * (i >> 2) + (i & 3) < rel) ? 0.f : pv;
           s[8 * j + i] = pv;
@@ -175,15 +173,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnParams p) 
         db[j] = pack8(dp, 8 * j);
       }
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          dv[dt] = mfma32(tr.read(Gs, RS, 32 * w + 16 * j, 32 * dt), pb[j], dv[dt]);
-          dk[dt] = mfma32(tr.read(Qs, RS, 32 * w + 16 * j, 32 * dt), db[j], dk[dt]);
+        for (int dt = 0; dt < D / 32; ++dt) {
+          dv[dt] = mfma32(tr.read(Gs, 32 * w + 16 * j, dt), pb[j], dv[dt]);
+          dk[dt] = mfma32(tr.read(Qs, 32 * w + 16 * j, dt), db[j], dk[dt]);
         }
-      }
     }
-    if (more) stash(buf ^ 1);
+    wait_vmem();
     __syncthreads();
   }
 
@@ -231,17 +228,26 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnParams p) 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnParams p) {
   constexpr int BM = kFwdBM, BN = kFwdBN, NT = 256;
-  using Tile = RowTile<BN, D, NT>;
-  constexpr int RS = Tile::RS, TSZ = BN * RS;
-  constexpr int STAGE = 2 * TSZ;  // Ks, Vs
+  using Tile = LdsTile<BN, D, NT / 64>;
+  constexpr int TE = Tile::ELEMS, STAGE = 2 * TE;  // K, V
   __shared__ __align__(16) bf16 smem[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int wu = wave_uniform(w);
+  Tile kt, vt;
+  kt.init(p.k_tok, lane);
+  vt.init(p.v_tok, lane);
+  RowRead<D> rr;
+  rr.init(lane);
+  TrRead<D> tr;
+  tr.init(lane);
+  const float c = p.scale_log2;
 
   const int2 tl = p.qtiles[blockIdx.x];
   if (tl.x < 0) return;
   const SeqInfo si = p.seq[tl.x];
   const int hqi = blockIdx.y, hk = hqi / p.n_rep;
   const int q0 = tl.y * BM;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int off = si.k_len - si.q_len;
   int kv_end = si.k_len;
   if (CAUSAL) kv_end = min(kv_end, q0 + BM + off);
@@ -270,32 +276,26 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnParams p) {
   f32x16 dq[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) dq[i] = zero16();
-  const float c = p.scale_log2;
 
   const bf16* kbase = p.k + (int64_t)si.k_start * p.k_tok + (int64_t)hk * p.k_head;
   const bf16* vbase = p.v + (int64_t)si.k_start * p.v_tok + (int64_t)hk * p.v_head;
-  Tile kt, vt;
-  kt.init(p.k_tok, tid);
-  vt.init(p.v_tok, tid);
-  TrRead tr;
-  tr.init(RS, lane);
   if (nblk > 0) {
-    kt.load(kbase, p.k_tok, si.k_len);
-    vt.load(vbase, p.v_tok, si.k_len);
-    kt.store(smem, tid);
-    vt.store(smem + TSZ, tid);
+    kt.issue(kbase, p.k_tok, si.k_len, smem, wu);
+    vt.issue(vbase, p.v_tok, si.k_len, smem + TE, wu);
   }
+  wait_vmem();
   __syncthreads();
 
   const int wq_last = q0 + 32 * w + 31;
   for (int kb = 0; kb < nblk; ++kb) {
     const bf16* Ks = smem + (kb & 1) * STAGE;
-    const bf16* Vs = Ks + TSZ;
+    const bf16* Vs = Ks + TE;
     const int k0 = kb * BN;
     const bool more = kb + 1 < nblk;
     if (more) {
-      kt.load(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN);
-      vt.load(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN);
+      bf16* nx = smem + ((kb + 1) & 1) * STAGE;
+      kt.issue(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN, nx, wu);
+      vt.issue(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN, nx + TE, wu);
     }
     const bool active = !CAUSAL || (k0 <= wq_last + off);
     if (active) {
@@ -306,14 +306,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnParams p) {
       for (int t = 0; t < BN / 32; ++t) {
         s[t] = zero16();
         dp[t] = zero16();
-        const bf16* kr = Ks + (32 * t + l32) * RS + 8 * h;
-        const bf16* vr = Vs + (32 * t + l32) * RS + 8 * h;
-#pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks) {
-          s[t] = mfma32(ld_bf16x8(kr + 16 * ks), qf[ks], s[t]);
-          dp[t] = mfma32(ld_bf16x8(vr + 16 * ks), gf[ks], dp[t]);
-        }
       }
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+        for (int t = 0; t < BN / 32; ++t) {
+          s[t] = mfma32(rr.read(Ks, 32 * t, ks), qf[ks], s[t]);
+          dp[t] = mfma32(rr.read(Vs, 32 * t, ks), gf[ks], dp[t]);
+        }
       const int rel = lim - k0 - 4 * h;
       bf16x8 db[BN / 16];
 #pragma unroll
@@ -328,16 +328,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnParams p) {
         db[2 * t + 1] = pack8(dp[t], 8);
       }
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
+      for (int st = 0; st < BN / 16; ++st)
 #pragma unroll
-        for (int st = 0; st < BN / 16; ++st) dq[dt] = mfma32(tr.read(Ks, RS, 16 * st, 32 * dt), db[st], dq[dt]);
-      }
+        for (int dt = 0; dt < D / 32; ++dt) dq[dt] = mfma32(tr.read(Ks, 16 * st, dt), db[st], dq[dt]);
     }
-    if (more) {
-      bf16* nx = smem + ((kb + 1) & 1) * STAGE;
-      kt.store(nx, tid);
-      vt.store(nx + TSZ, tid);
-    }
+    wait_vmem();
     __syncthreads();
   }
 

@@ -16,9 +16,9 @@
 // scores of ONE q row: the online-softmax max is in-lane plus one cross-half
 // swap.  P^T then feeds O^T += V^T P^T straight from registers, with V^T read
 // from the row-major V tile by ds_read_b64_tr_b16 in the row order of the
-// score accumulators (no shuffles).  K and V tiles of 64 kv
-// rows are double-buffered in LDS; the next tile's global loads are in flight
-// while the current one is multiplied.
+// score accumulators (no shuffles).  K and V tiles of 64 kv rows are
+// double-buffered in LDS and staged with direct global->LDS loads: the next
+// tile is in flight while the current one is multiplied, at no register cost.
 //
 // Rescaling is lazy: a row's reference max only moves when a block's max
 // exceeds it by more than 2^8 (so unnormalised P stays <= 256, exact in the
@@ -35,16 +35,26 @@ constexpr float kRescaleLog2 = 8.f;
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   constexpr int BM = kFwdBM, BN = kFwdBN, NT = 256;
-  using Tile = RowTile<BN, D, NT>;
-  constexpr int RS = Tile::RS, TSZ = BN * RS, STAGE = 2 * TSZ;
+  using Tile = LdsTile<BN, D, NT / 64>;
+  constexpr int TE = Tile::ELEMS, STAGE = 2 * TE;  // K, V
   __shared__ __align__(16) bf16 smem[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int wu = wave_uniform(w);
+  Tile kt, vt;
+  kt.init(p.k_tok, lane);
+  vt.init(p.v_tok, lane);
+  RowRead<D> rr;
+  rr.init(lane);
+  TrRead<D> tr;
+  tr.init(lane);
+  const float c = p.scale_log2;
 
   const int2 tl = p.qtiles[blockIdx.x];
   if (tl.x < 0) return;
   const SeqInfo si = p.seq[tl.x];
   const int hqi = blockIdx.y, hk = hqi / p.n_rep;
   const int q0 = tl.y * BM;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int off = si.k_len - si.q_len;
   int kv_end = si.k_len;
   if (CAUSAL) kv_end = min(kv_end, q0 + BM + off);
@@ -67,42 +77,49 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) oacc[i] = zero16();
   float mref = -INFINITY, lsum = 0.f;  // reference max (log2 units), per-half partial row sum
-  const float c = p.scale_log2;
 
   const bf16* kbase = p.k + (int64_t)si.k_start * p.k_tok + (int64_t)hk * p.k_head;
   const bf16* vbase = p.v + (int64_t)si.k_start * p.v_tok + (int64_t)hk * p.v_head;
-  Tile kt, vt;
-  kt.init(p.k_tok, tid);
-  vt.init(p.v_tok, tid);
-  TrRead tr;
-  tr.init(RS, lane);
   if (nblk > 0) {
-    kt.load(kbase, p.k_tok, si.k_len);
-    vt.load(vbase, p.v_tok, si.k_len);
-    kt.store(smem, tid);
-    vt.store(smem + TSZ, tid);
+    kt.issue(kbase, p.k_tok, si.k_len, smem, wu);
+    vt.issue(vbase, p.v_tok, si.k_len, smem + TE, wu);
   }
+  wait_vmem();
   __syncthreads();
 
   const int wq_last = q0 + 32 * w + 31;  // last q row of this wave
   for (int kb = 0; kb < nblk; ++kb) {
     const bf16* Ks = smem + (kb & 1) * STAGE;
-    const bf16* Vs = Ks + TSZ;
+    const bf16* Vs = Ks + TE;
     const int k0 = kb * BN;
     const bool more = kb + 1 < nblk;
     if (more) {
-      kt.load(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN);
-      vt.load(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN);
+      bf16* nx = smem + ((kb + 1) & 1) * STAGE;
+      kt.issue(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN, nx, wu);
+      vt.issue(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN, nx + TE, wu);
     }
     const bool active = !CAUSAL || (k0 <= wq_last + off);
     if (active) {
+      // independent accumulators innermost, so consecutive MFMAs never wait on each other
       f32x16 s[BN / 32];
 #pragma unroll
-      for (int t = 0; t < BN / 32; ++t) {
-        s[t] = zero16();
-        const bf16* kr = Ks + (32 * t + l32) * RS + 8 * h;
+      for (int t = 0; t < BN / 32; ++t) s[t] = zero16();
+      // software pipeline: operand reads run two k-steps ahead of the MFMAs
+      constexpr int KS = D / 16, NTL = BN / 32;
+      bf16x8 ka[KS][NTL];
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks) s[t] = mfma32(ld_bf16x8(kr + 16 * ks), qf[ks], s[t]);
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int t = 0; t < NTL; ++t) ka[ks][t] = rr.read(Ks, 32 * t, ks);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int t = 0; t < NTL; ++t) s[t] = mfma32(ka[ks][t], qf[ks], s[t]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * NTL, 0);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 2 < KS) __builtin_amdgcn_sched_group_barrier(0x100, NTL, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NTL, 0);
       }
       // accumulator (t, r) holds kv = k0 + 32t + nrow(r, h)
       const bool need_mask = (k0 + BN > si.k_len) || (CAUSAL && k0 + BN - 1 > q0 + 32 * w + off);
@@ -144,16 +161,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
       }
       lsum += ps;
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
+      for (int st = 0; st < BN / 16; ++st)
 #pragma unroll
-        for (int st = 0; st < BN / 16; ++st) oacc[dt] = mfma32(tr.read(Vs, RS, 16 * st, 32 * dt), pb[st], oacc[dt]);
-      }
+        for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = mfma32(tr.read(Vs, 16 * st, dt), pb[st], oacc[dt]);
     }
-    if (more) {
-      bf16* nx = smem + ((kb + 1) & 1) * STAGE;
-      kt.store(nx, tid);
-      vt.store(nx + TSZ, tid);
-    }
+    wait_vmem();
     __syncthreads();
   }
 
@@ -180,18 +192,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
 
 }  // namespace
 
-hipError_t launch_attn_fwd(const AttnParams& p, int d, int causal, int qcap, hipStream_t stream) {
-  const dim3 grid(qcap, p.hq), block(256);
-  if (d == 128) {
-    if (causal) hipLaunchKernelGGL((attn_fwd_kernel<128, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((attn_fwd_kernel<128, false>), grid, block, 0, stream, p);
-  } else if (d == 64) {
-    if (causal) hipLaunchKernelGGL((attn_fwd_kernel<64, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((attn_fwd_kernel<64, false>), grid, block, 0, stream, p);
-  } else {
-    return hipErrorInvalidValue;
-  }
+template <int D, bool CAUSAL>
+hipError_t launch_fwd_t(const AttnParams& p, int qcap, hipStream_t stream) {
+  hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL>), dim3(qcap, p.hq), dim3(256), 0, stream, p);
   return hipGetLastError();
+}
+
+hipError_t launch_attn_fwd(const AttnParams& p, int d, int causal, int qcap, hipStream_t stream) {
+  if (d == 128) return causal ? launch_fwd_t<128, true>(p, qcap, stream) : launch_fwd_t<128, false>(p, qcap, stream);
+  if (d == 64) return causal ? launch_fwd_t<64, true>(p, qcap, stream) : launch_fwd_t<64, false>(p, qcap, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace siq

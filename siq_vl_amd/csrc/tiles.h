@@ -1,123 +1,137 @@
-// Global -> LDS staging of [rows x D] bf16 tiles and the transposed LDS
-// operand read, shared by the attention kernels.
+// Global -> LDS staging of [rows x D] bf16 tiles and the MFMA operand reads
+// from them, shared by the attention kernels.
 //
-// Tiles are always stored row-major in LDS and never transposed in registers:
-// an MFMA operand that needs k along the tile rows (V^T, K^T, Q^T, dO^T) is
-// read with ds_read_b64_tr_b16 (gfx950).
+// Staging uses gfx950's direct loads (global_load_lds_dwordx4): each wave
+// instruction moves 64 x 16 bytes from global memory straight into 1 KB of
+// contiguous LDS (lane l's chunk at byte 16 l), with no VGPRs in between, so
+// the next tile can be in flight while the current one is multiplied without
+// spending registers on it.
 //
-// Row padding (kRowPad): a quarter-wave reads 16 B from each of 16 rows for
-// the row-major operand, and 32 B from each of 4 consecutive rows for the
-// transposed one.  With 64 four-byte banks both are conflict-free when the row
-// stride is 12 dwords mod 64 (D = 128: 64 + 12) or 52 (D = 64: 32 + 20):
-// 16 rows land on 16 distinct 4-bank groups and 4 rows on 4 disjoint 8-bank
-// spans.
+// LDS layout: rows are D bf16 long with no padding; within row r the 16-byte
+// chunk c is stored at chunk position c ^ swz(r).  Two read patterns must be
+// bank-conflict free (64 banks of 4 bytes):
+//  * row operand (ds_read_b128): a quarter-wave reads one chunk from each of
+//    16 consecutive rows -> swz must be a bijection on (r mod 16) for D = 128
+//    (a 256-byte row spans all banks) and on (r mod 2, chunk) for D = 64;
+//  * transposed operand (ds_read_b64_tr_b16): a quarter-wave reads the chunk
+//    pair (2a, 2a + 1) of 4 consecutive rows -> the 4 pairs must be disjoint.
+// D = 128: swz(r) = 2 (r mod 8) + bit3(r);  D = 64: swz(r) = 2 (bits 1-2 of r) + bit3(r).
 #pragma once
 #include "common.h"
 
 namespace siq {
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <int D>
-struct RowPad;
-template <>
-struct RowPad<128> {
-  static constexpr int value = 24;  // elements: 12 dwords
-};
-template <>
-struct RowPad<64> {
-  static constexpr int value = 40;  // elements: 20 dwords
-};
+__device__ __forceinline__ int swz(int r) {
+  static_assert(D == 128 || D == 64, "head dim");
+  if (D == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+  return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
+}
 
-// Row-major staging.  One unit = one 16-byte chunk; consecutive lanes take
-// consecutive chunks of a row, so a wave's load instruction reads whole rows.
-// Each thread keeps the 32-bit element offset of its chunks (fixed for the
-// whole kernel); full tiles load with uniform base + offset, tail tiles read
-// the last valid row instead of rows past the end (always in bounds) and
-// replace them by zeros with a select, so no load is predicated.
-template <int ROWS, int D, int NT>
-struct RowTile {
+__device__ __forceinline__ int wave_uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Direct staging of a ROWS x D tile by the NW waves of a workgroup.  Wave w
+// issues instructions w*PERW .. w*PERW + PERW - 1; instruction i covers rows
+// [i*RPI, (i+1)*RPI) (1 KB, 64 chunks), lane l taking row i*RPI + l / CH and
+// chunk position l % CH.  The swizzle repeats every 16 rows, so a lane only
+// keeps PAT = 16 / RPI base offsets; the rest is a uniform row shift.  Rows
+// >= nrows load the last valid row instead (always in bounds; consumers mask
+// those rows or multiply them by exact zeros).
+template <int ROWS, int D, int NW>
+struct LdsTile {
   static constexpr int CH = D / 8;
-  static constexpr int UNITS = ROWS * CH;
-  static constexpr int PER = (UNITS + NT - 1) / NT;
-  static constexpr int RS = D + RowPad<D>::value;
-  static_assert(UNITS % NT == 0, "every thread stages the same number of chunks");
+  static constexpr int RPI = 64 / CH;          // rows per wave instruction
+  static constexpr int NINSTR = ROWS / RPI;
+  static constexpr int PERW = NINSTR / NW;
+  static constexpr int PAT = 16 / RPI;          // distinct swizzle patterns
+  static constexpr int ELEMS = ROWS * D;
+  static_assert(NINSTR % NW == 0 && PERW % PAT == 0, "tile splits evenly over the waves");
 
-  u32x4 v[PER];
-  uint32_t off[PER];  // element offset of chunk i inside the tile
-  int row[PER];
+  uint32_t base[PAT];  // element offset of this lane's chunk for instruction p (p < PAT), row shift excluded
+  int lrow;            // row of this lane inside an instruction
 
-  __device__ __forceinline__ void init(int64_t stride, int tid) {
+  __device__ __forceinline__ void init(int64_t stride, int lane) {
+    lrow = lane / CH;
+    const int pc = lane % CH;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = tid + i * NT;
-      const int c = u % CH, r = u / CH;
-      row[i] = r;
-      off[i] = (uint32_t)(r * stride + 8 * c);
+    for (int pi = 0; pi < PAT; ++pi) {
+      const int r = pi * RPI + lrow;
+      base[pi] = (uint32_t)(r * stride + 8 * (pc ^ swz<D>(r)));
     }
   }
 
-  // base: (row 0, col 0) of the tile in global memory; rows >= nrows become 0.
-  __device__ __forceinline__ void load(const bf16* base, int64_t stride, int nrows) {
-    if (nrows >= ROWS) {
+  // gbase: (row 0, col 0) of the tile in global memory; lds: the tile's LDS
+  // base; wu: this wave's index (wave-uniform).
+  __device__ __forceinline__ void issue(const bf16* gbase, int64_t stride, int nrows, bf16* lds, int wu) const {
 #pragma unroll
-      for (int i = 0; i < PER; ++i) v[i] = *reinterpret_cast<const u32x4*>(base + off[i]);
-      return;
-    }
-    if (nrows <= 0) {
-#pragma unroll
-      for (int i = 0; i < PER; ++i) v[i] = u32x4{0u, 0u, 0u, 0u};
-      return;
-    }
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int r = row[i];
-      const uint32_t o = r < nrows ? off[i] : off[i] - (uint32_t)((r - nrows + 1) * stride);
-      const u32x4 x = *reinterpret_cast<const u32x4*>(base + o);
-      v[i] = r < nrows ? x : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-
-  __device__ __forceinline__ void store(bf16* s, int tid) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = tid + i * NT;
-      const int c = u % CH, r = u / CH;
-      *reinterpret_cast<u32x4*>(s + r * RS + 8 * c) = v[i];
+    for (int k = 0; k < PERW; ++k) {
+      const int i = wu * PERW + k;
+      const int r0 = (i - (k % PAT)) * RPI;  // uniform row shift (multiple of 16)
+      uint32_t o = base[k % PAT] + (uint32_t)(r0 * stride);
+      if (nrows < ROWS) {
+        const int r = i * RPI + lrow;
+        o = r < nrows ? o : o - (uint32_t)((r - nrows + 1) * stride);
+      }
+      __builtin_amdgcn_global_load_lds(gbase + o, (lds_void*)(lds + i * 512), 16, 0, 0);
     }
   }
 };
 
-// Transposed MFMA operand from a row-major LDS tile T[k][m] (row stride rs).
-// ds_read_b64_tr_b16: within each 16-lane group, lane p = 4j + q supplies the
-// address of row j of a 4 x 16 block (8 bytes at column group q) and lane i
-// receives element i % 4 of the chunks supplied by lanes 4j + i / 4, j = 0..3,
-// i.e. 4 consecutive rows of one column.  Two reads give 8 k values.
-//
-// TrRead precomputes the lane-dependent part once.  read(T, k0, m0) returns for
-// lane l the values T[k0 + krow(i, h)][m0 + perm32(l % 32)], i = 0..7, with
-//   krow(i, h) = 4h + i        (i < 4),   8 + 4h + (i - 4)   (i >= 4),
-// which is exactly the row order r -> 8*(r/4) + 4h + (r%4) of an MFMA D tile:
-// P or dS taken from accumulators 8j..8j+7 pairs with the tr read at k0 + 16j.
-// The column permutation perm32 (chosen per supplying lane) makes the product's
-// rows come out as 8 consecutive m per accumulator group.
-struct TrRead {
-  int base;  // element offset of this lane's first supplied address
-  __device__ __forceinline__ void init(int rs, int lane) {
-    const int G = lane >> 4, p = lane & 15, j = p >> 2, q = p & 3;
-    const int col = 16 * (G & 1) + 8 * (q & 1) + 4 * (q >> 1);
-    base = (4 * (G >> 1) + j) * rs + col;
+// Row operand reads: lane l reads row (rbase + l % 32), logical chunk
+// 2 ks + h (d = 16 ks + 8 h .. +7), for ks = 0 .. D/16 - 1.  The swizzled chunk
+// offsets depend only on (l % 32) because row bases are multiples of 32.
+template <int D>
+struct RowRead {
+  uint32_t off[D / 16];  // element offsets within a 32-row block
+  __device__ __forceinline__ void init(int lane) {
+    const int l32 = lane & 31, h = lane >> 5, f = swz<D>(l32);
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) off[ks] = (uint32_t)(l32 * D + (((2 * ks + h) ^ f) << 3));
   }
-  __device__ __forceinline__ bf16x8 read(const bf16* T, int rs, int k0, int m0) const {
-    const bf16* a = T + base + k0 * rs + m0;
-    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)a);
-    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(a + 8 * rs));
+  // T: tile base, rb: first row of the 32-row block (multiple of 32)
+  __device__ __forceinline__ bf16x8 read(const bf16* T, int rb, int ks) const { return ld_bf16x8(T + rb * D + off[ks]); }
+};
+
+// Transposed operand reads with ds_read_b64_tr_b16.  Within each 16-lane
+// group, lane p = 4j + q supplies the address of row j of a 4 x 16 block
+// (8 bytes at column group q) and lane i receives element i % 4 of the chunks
+// supplied by lanes 4j + i / 4 (j = 0..3): 4 consecutive rows of one column.
+// read(T, k0, dt) returns for lane l the values
+//   T[k0 + krow(i, h)][32 dt + perm32(l % 32)],  i = 0..7,
+//   krow(i, h) = 4h + i (i < 4), 8 + 4h + (i - 4) (i >= 4),
+// which is the row order r -> 8 (r/4) + 4h + (r%4) of an MFMA D tile: P or dS
+// taken from accumulators 8j..8j+7 pairs with the read at k0 + 16 j.  The
+// column permutation perm32 (chosen per supplying lane) makes the product's
+// rows come out as 8 consecutive d per accumulator group.  k0 must be a
+// multiple of 16.
+template <int D>
+struct TrRead {
+  uint32_t off[2][D / 32];
+  __device__ __forceinline__ void init(int lane) {
+    const int G = lane >> 4, p = lane & 15, j = p >> 2, q = p & 3;
+    const int cl = 2 * (G & 1) + (q & 1);  // logical chunk within a 32-column block
+    const int wo = 4 * (q >> 1);           // element offset inside the chunk
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int r = 4 * (G >> 1) + j + 8 * e;
+      const int f = swz<D>(r);
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) off[e][dt] = (uint32_t)(r * D + (((4 * dt + cl) ^ f) << 3) + wo);
+    }
+  }
+  __device__ __forceinline__ bf16x8 read(const bf16* T, int k0, int dt) const {
+    const bf16* base = T + k0 * D;
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + off[0][dt]));
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + off[1][dt]));
     return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
 };
 
-// Natural (unpermuted) D-tile row of accumulator r in lane half h.
-__device__ __forceinline__ constexpr int nrow(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+// Wait for this wave's outstanding global (and direct-to-LDS) loads.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Per-sequence extents, clamped on the device to [0, total).
 struct SeqInfo {
