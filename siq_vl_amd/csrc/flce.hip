@@ -28,88 +28,188 @@ namespace siq {
 
 namespace {
 
-constexpr int BI = 256, BJ = 256, BK = 32, NT = 256;
-constexpr int LS = BK + 8;          // LDS row stride of a staged [256][32] operand tile
-constexpr int TILE_EL = 256 * LS;   // bf16 elements per staged operand
+constexpr int BI = 256, BJ = 256, BK = 64, NT = 256;
+constexpr int SLAB = 256 * BK;      // bf16 elements of one staged operand slab (32 KB)
 constexpr int kVT = BI;             // vocab columns per logits tile
 constexpr int kXcds = 8;
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
 struct GOp {
   const bf16* base;
   int64_t ld, rows, cols;  // element (r, c) at base[r * ld + c]; 16-byte chunks along c
 };
 
-// One 4-row x 8-column unit (global layout) per thread, staged into a
-// k-contiguous [256][32] LDS tile.  KC: the tile's k runs along the global
-// column (row-major store); otherwise along the global row (transposed store).
+// Operand slabs live in LDS in one of two orientations, both XOR-swizzled at
+// 16-byte granularity so the MFMA operand reads are bank-conflict free (64
+// banks of 4 bytes):
+//  * KC ("k contiguous"): [256 rows][64 k], 128-byte rows; the slab's rows are
+//    the operand's M (or N) index.  Read as row operands (one chunk from each
+//    of 16 consecutive rows per quarter-wave): swz_kc spreads 16 rows over
+//    distinct (bank half, chunk) pairs.
+//  * NKC: [64 k][256 cols], 512-byte rows; the slab's columns are the operand's
+//    M (or N) index.  Read with ds_read_b64_tr_b16 (a chunk pair from each of 4
+//    consecutive rows per quarter-wave): swz_nkc makes the 4 pairs disjoint.
+__device__ __forceinline__ int swz_kc(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
+__device__ __forceinline__ int swz_nkc(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+
+// Direct global->LDS staging of one slab: 32 instructions of 1 KB, 8 per wave.
+// Rows / chunks past the operand's extent re-read the last valid one (always in
+// bounds); the garbage that produces is either never stored (M/N tails) or
+// multiplied by rows the B-operand pass zeroes (K tails).
 template <bool KC>
-struct Stage {
-  u32x4 v[4];
-  int c, g;
-  int64_t grow, gcol;  // global origin of this thread's unit
-  __device__ __forceinline__ void init(int tid) {
+struct SlabLoad {
+  int lrow, lpc;  // this lane's row inside an instruction and physical chunk
+  int wrow;       // first slab row of this wave's 8 instructions
+  uint32_t off0, off1;  // KC: element offsets of instructions k = 0, 1 (k + 2 adds 16 rows)
+  __device__ __forceinline__ void init(const GOp& op, int lane, int w) {
     if (KC) {
-      c = tid % (BK / 8);
-      g = tid / (BK / 8);
+      lrow = lane / 8;
+      lpc = lane % 8;
+      wrow = 64 * w;   // instruction i = 8w + k covers rows 8i .. 8i + 7
+      const int r0 = wrow + lrow, r1 = wrow + 8 + lrow;
+      off0 = (uint32_t)(r0 * op.ld + 8 * (lpc ^ swz_kc(r0)));
+      off1 = (uint32_t)(r1 * op.ld + 8 * (lpc ^ swz_kc(r1)));
     } else {
-      g = tid % (BK / 4);
-      c = tid / (BK / 4);
+      lrow = lane / 32;
+      lpc = lane % 32;
+      wrow = 16 * w;   // instruction i = 8w + k covers rows 2i, 2i + 1
+      off0 = off1 = 0;
     }
   }
-  __device__ __forceinline__ void load(const GOp& op, int64_t r0, int64_t k0) {
-    if (KC) {
-      grow = r0 + 4 * g;
-      gcol = k0 + 8 * c;
-    } else {
-      grow = k0 + 4 * g;
-      gcol = r0 + 8 * c;
+  // r0: first M/N index of the tile, k0: first k of the slab
+  __device__ __forceinline__ void issue(const GOp& op, int64_t r0, int64_t k0, bf16* lds, int wu) const {
+    const bool full = KC ? (r0 + 256 <= op.rows && k0 + BK <= op.cols) : (k0 + BK <= op.rows && r0 + 256 <= op.cols);
+    if (full) {
+      // uniform slab base + 32-bit per-lane offsets (every offset < 2^31: rows < 256 x ld or k < 64 x ld)
+      const bf16* base = KC ? op.base + r0 * op.ld + k0 : op.base + k0 * op.ld + r0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        uint32_t o;
+        if (KC) {
+          o = ((k & 1) ? off1 : off0) + (uint32_t)(16 * (k >> 1) * op.ld);
+        } else {
+          const int r = wrow + 2 * k + lrow;
+          o = (uint32_t)(r * op.ld + 8 * (lpc ^ swz_nkc(r)));
+        }
+        __builtin_amdgcn_global_load_lds(base + o, (lds_void*)(lds + (wu * 8 + k) * 512), 16, 0, 0);
+      }
+      return;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool ok = (grow + j < op.rows) && (gcol < op.cols);
-      v[j] = ok ? *reinterpret_cast<const u32x4*>(op.base + (grow + j) * op.ld + gcol) : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-  __device__ __forceinline__ void store(bf16* s) const {
-    if (KC) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(s + (4 * g + j) * LS + 8 * c) = v[j];
-    } else {
-      u32x2 cols[8];
-      transpose4x8(v, cols);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x2*>(s + (8 * c + j) * LS + 4 * g) = cols[j];
+    for (int k = 0; k < 8; ++k) {
+      const int r = KC ? wrow + 8 * k + lrow : wrow + 2 * k + lrow;
+      const int c = KC ? (lpc ^ swz_kc(r)) : (lpc ^ swz_nkc(r));
+      int64_t gr = KC ? r0 + r : k0 + r;
+      int64_t gc = KC ? k0 + 8 * c : r0 + 8 * c;
+      gr = gr < op.rows ? gr : op.rows - 1;
+      gc = gc < op.cols ? gc : op.cols - 8;
+      __builtin_amdgcn_global_load_lds(op.base + gr * op.ld + gc, (lds_void*)(lds + (wu * 8 + k) * 512), 16, 0,
+                                       0);
     }
   }
 };
 
-// dZ from E on the fly: rows = chunk tokens, cols = vocab.
+// MFMA operand reads of the wave's 128-row block of a slab (4 tiles of 32):
+// returns for lane l the 8 k values (16 ks + 8 h + i, i = 0..7) of operand row
+// 32 t + rowmap(l % 32), with rowmap = perm32 when PERM (A operands: the
+// product's rows then come out as 8 consecutive indices per accumulator
+// group) and the identity otherwise (B operands).
+template <bool KC, bool PERM>
+struct SlabRead {
+  uint32_t off[4][2];  // KC: [ks][-]; NKC: [t][e]
+  int rowb;
+  __device__ __forceinline__ void init(int lane, int wblock) {
+    const int l32 = lane & 31, h = lane >> 5;
+    if (KC) {
+      const int r = 128 * wblock + (PERM ? perm32(l32) : l32);
+      const int f = swz_kc(r);
+      rowb = r * BK;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) off[ks][0] = (uint32_t)(rowb + (((2 * ks + h) ^ f) << 3));
+    } else {
+      const int G = lane >> 4, p = lane & 15, j = p >> 2, q = p & 3;
+      const int cs = PERM ? 16 * (G & 1) + 8 * (q & 1) + 4 * (q >> 1) : 16 * (G & 1) + 4 * q;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int r = 8 * (G >> 1) + j + 4 * e;  // row within a 16-row k group
+        const int f = swz_nkc(r);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int col = 128 * wblock + 32 * t + cs;
+          off[t][e] = (uint32_t)(r * 256 + ((((col >> 3) & 15) ^ f) << 3) + ((col >> 7) << 7) + (col & 7));
+        }
+      }
+    }
+  }
+  __device__ __forceinline__ bf16x8 read(const bf16* S, int t, int ks) const {
+    if (KC) return ld_bf16x8(S + off[ks][0] + t * 32 * BK);
+    const bf16* base = S + ks * 16 * 256;
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + off[t][0]));
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + off[t][1]));
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+};
+
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// dZ from the exp-normalised logits chunk E, applied to a B slab in LDS after
+// it lands: dZ = E * f[tok, tile] - g[tok] * [v == y[tok]], zero for token rows
+// past the chunk and vocab columns past V.  Each thread owns one token row of
+// the slab (KC: a whole 64-column row; NKC: a quarter of a 256-column row).
 struct DzForm {
   const float* f;        // [C, nvt]
   const float* g;        // [C]
   const int64_t* y;      // [C] labels of the chunk
   int64_t nvt, nc, vocab;
-  __device__ __forceinline__ void apply(u32x4 (&v)[4], int64_t tok0, int64_t v0) const {
-    if (v0 >= vocab) return;  // zero-filled padding columns: no factor to apply
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t t = tok0 + j;
-      if (t >= nc) continue;
-      const float fv = f[t * nvt + v0 / kVT];
-      const float gv = g[t];
-      const int64_t yv = y[t];
-      bf16x8 e = __builtin_bit_cast(bf16x8, v[j]);
-      bf16x8 o;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float d = (float)e[i] * fv;
-        if (v0 + i == yv) d -= gv;
-        o[i] = (bf16)d;
-      }
-      v[j] = __builtin_bit_cast(u32x4, o);
-    }
-  }
 };
+
+template <bool KC>
+__device__ __forceinline__ void dz_pass(const DzForm& F, bf16* S, int64_t j0, int64_t k0, int tid) {
+  int r, c0;
+  int64_t tok, vbase;
+  if (KC) {  // [256 tok][64 v]: J = tok, k = v
+    r = tid;
+    c0 = 0;
+    tok = j0 + r;
+    vbase = k0;
+  } else {   // [64 tok][256 v]: k = tok, J = v
+    r = tid >> 2;
+    c0 = (tid & 3) * 8;
+    tok = k0 + r;
+    vbase = j0;
+  }
+  const bool tv = tok < F.nc;
+  const int64_t tile = (KC ? k0 : j0) / kVT;
+  const float fv = tv ? F.f[tok * F.nvt + tile] : 0.f;
+  const float gv = tv ? F.g[tok] : 0.f;
+  // label and vocabulary end relative to this thread's first column (32-bit)
+  const int64_t yrel64 = tv ? F.y[tok] - vbase : -1;
+  const int yrel = (yrel64 >= 0 && yrel64 < 256) ? (int)yrel64 : -1;
+  const int64_t vend64 = F.vocab - vbase;
+  const int vend = vend64 > 256 ? 256 : (int)vend64;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int pc = c0 + k;
+    const int c = KC ? (pc ^ swz_kc(r)) : (pc ^ swz_nkc(r));
+    bf16* ptr = S + (KC ? r * BK : r * 256) + pc * 8;
+    const bf16x8 e = ld_bf16x8(ptr);
+    bf16x8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (bf16)((float)e[i] * fv);
+    const int cb = 8 * c;
+    if (yrel - cb >= 0 && yrel - cb < 8) {  // the label column (one chunk per valid row)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = (i == yrel - cb) ? (bf16)((float)e[i] * fv - gv) : o[i];
+    }
+    if (cb + 8 > vend) {  // columns past the vocabulary (last tile only)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = cb + i < vend ? o[i] : (bf16)0.f;
+    }
+    st_bf16x8(ptr, o);
+  }
+}
 
 // Maps a 1-D block id onto (I tile, J tile) so that the blocks sharing the
 // big operand tile run back to back on one XCD (block b is dispatched to XCD
@@ -131,62 +231,69 @@ __device__ __forceinline__ bool tile_of(int nI, int nJ, int& ti, int& tj) {
   return true;
 }
 
-// C[i][j] = sum_k A[i][k] B[j][k] over k in [kb, ke) with 4 waves of
-// 128x128 (4x4 MFMA 32x32 tiles).  acc[ti][tj][r] holds
-// i = i0 + 128*wi + 32*ti + drow(r, h), j = j0 + 128*wj + 32*tj + l32.
+// C[i][j] = sum_k A[i][k] B[j][k] over k in [kb, ke) (kb, ke multiples of BK
+// except ke at the operand's end) with 4 waves of 128x128 (4x4 MFMA 32x32
+// tiles).  acc[ti][tj][r] holds i = i0 + 128*wi + 32*ti + drow(r, h),
+// j = j0 + 128*wj + 32*tj + l32.  With BFORM the B slab is turned into dZ in
+// LDS after it lands.
 template <bool AKC, bool BKC, bool BFORM>
 __device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B, const DzForm& form, int64_t i0,
                                           int64_t j0, int64_t kb, int64_t ke, f32x16 (&acc)[4][4]) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wi = w & 1, wj = w >> 1;
-  Stage<AKC> sa;
-  Stage<BKC> sb;
-  sa.init(tid);
-  sb.init(tid);
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  SlabLoad<AKC> la;
+  SlabLoad<BKC> lb;
+  la.init(A, lane, w);
+  lb.init(B, lane, w);
+  SlabRead<AKC, true> ra;
+  SlabRead<BKC, false> rb;
+  ra.init(lane, wi);
+  rb.init(lane, wj);
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = zero16();
   const int nk = ke > kb ? (int)((ke - kb + BK - 1) / BK) : 0;
-  auto fetch = [&](int it) {
-    const int64_t k0 = kb + (int64_t)it * BK;
-    sa.load(A, i0, k0);
-    sb.load(B, j0, k0);
-    if (BFORM) {
-      if (BKC) form.apply(sb.v, sb.grow, sb.gcol);
-      else form.apply(sb.v, sb.grow, sb.gcol);
-    }
-  };
   if (nk > 0) {
-    fetch(0);
-    sa.store(smem);
-    sb.store(smem + TILE_EL);
+    la.issue(A, i0, kb, smem, wu);
+    lb.issue(B, j0, kb, smem + SLAB, wu);
   }
+  wait_vmem();
   __syncthreads();
+  if (BFORM && nk > 0) {
+    dz_pass<BKC>(form, smem + SLAB, j0, kb, tid);
+    __syncthreads();
+  }
   for (int it = 0; it < nk; ++it) {
-    const bf16* As = smem + (it & 1) * 2 * TILE_EL;
-    const bf16* Bs = As + TILE_EL;
+    const bf16* As = smem + (it & 1) * 2 * SLAB;
+    const bf16* Bs = As + SLAB;
     const bool more = it + 1 < nk;
-    if (more) fetch(it + 1);
+    bf16* nx = smem + ((it + 1) & 1) * 2 * SLAB;
+    const int64_t kn = kb + (int64_t)(it + 1) * BK;
+    if (more) {
+      la.issue(A, i0, kn, nx, wu);
+      lb.issue(B, j0, kn, nx + SLAB, wu);
+    }
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8 af[4], bfr[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        af[t] = ld_bf16x8(As + (128 * wi + 32 * t + perm32(l32)) * LS + 16 * ks + 8 * h);
-        bfr[t] = ld_bf16x8(Bs + (128 * wj + 32 * t + l32) * LS + 16 * ks + 8 * h);
+        af[t] = ra.read(As, t, ks);
+        bfr[t] = rb.read(Bs, t, ks);
       }
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = mfma32(af[a], bfr[b], acc[a][b]);
     }
-    if (more) {
-      bf16* nx = smem + ((it + 1) & 1) * 2 * TILE_EL;
-      sa.store(nx);
-      sb.store(nx + TILE_EL);
-    }
+    wait_vmem();
     __syncthreads();
+    if (BFORM && more) {
+      dz_pass<BKC>(form, nx + SLAB, j0, kn, tid);
+      __syncthreads();
+    }
   }
 }
 
@@ -203,7 +310,7 @@ struct LogitsArgs {
 };
 
 __global__ __launch_bounds__(256) void flce_logits_kernel(const LogitsArgs p) {
-  __shared__ __align__(16) bf16 smem[4 * TILE_EL];
+  __shared__ __align__(16) bf16 smem[4 * SLAB];
   int ti, tj;
   if (!tile_of<true>(p.nI, p.nJ, ti, tj)) return;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
@@ -327,7 +434,7 @@ struct DhArgs {
 };
 
 __global__ __launch_bounds__(256) void flce_dh_kernel(const DhArgs p) {
-  __shared__ __align__(16) bf16 smem[4 * TILE_EL];
+  __shared__ __align__(16) bf16 smem[4 * SLAB];
   int ti, tj;
   if (!tile_of<false>(p.nI, p.nJ, ti, tj)) return;
   const int split = blockIdx.y;
@@ -401,7 +508,7 @@ struct DwArgs {
 };
 
 __global__ __launch_bounds__(256) void flce_dw_kernel(const DwArgs p) {
-  __shared__ __align__(16) bf16 smem[4 * TILE_EL];
+  __shared__ __align__(16) bf16 smem[4 * SLAB];
   int ti, tj;
   if (!tile_of<false>(p.nI, p.nJ, ti, tj)) return;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
