@@ -28,7 +28,8 @@ namespace siq {
 
 namespace {
 
-constexpr int BI = 256, BJ = 256, BK = 64, NT = 256;
+constexpr int BI = 256, BJ = 256, BK = 64, NT = 512;
+constexpr int NW = NT / 64;         // 8 waves: 2 along I (128 rows each) x 4 along J (64 cols each)
 constexpr int SLAB = 256 * BK;      // bf16 elements of one staged operand slab (32 KB)
 constexpr int kVT = BI;             // vocab columns per logits tile
 constexpr int kXcds = 8;
@@ -60,21 +61,22 @@ __device__ __forceinline__ int swz_nkc(int r) { return ((r & 7) << 1) | ((r >> 3
 // multiplied by rows the B-operand pass zeroes (K tails).
 template <bool KC>
 struct SlabLoad {
+  static constexpr int PERW = 32 / NW;  // instructions per wave (32 per slab)
   int lrow, lpc;  // this lane's row inside an instruction and physical chunk
-  int wrow;       // first slab row of this wave's 8 instructions
+  int wrow;       // first slab row of this wave's instructions
   uint32_t off0, off1;  // KC: element offsets of instructions k = 0, 1 (k + 2 adds 16 rows)
   __device__ __forceinline__ void init(const GOp& op, int lane, int w) {
     if (KC) {
       lrow = lane / 8;
       lpc = lane % 8;
-      wrow = 64 * w;   // instruction i = 8w + k covers rows 8i .. 8i + 7
+      wrow = 8 * PERW * w;   // instruction i = PERW w + k covers rows 8i .. 8i + 7
       const int r0 = wrow + lrow, r1 = wrow + 8 + lrow;
       off0 = (uint32_t)(r0 * op.ld + 8 * (lpc ^ swz_kc(r0)));
       off1 = (uint32_t)(r1 * op.ld + 8 * (lpc ^ swz_kc(r1)));
     } else {
       lrow = lane / 32;
       lpc = lane % 32;
-      wrow = 16 * w;   // instruction i = 8w + k covers rows 2i, 2i + 1
+      wrow = 2 * PERW * w;   // instruction i = PERW w + k covers rows 2i, 2i + 1
       off0 = off1 = 0;
     }
   }
@@ -85,7 +87,7 @@ struct SlabLoad {
       // uniform slab base + 32-bit per-lane offsets (every offset < 2^31: rows < 256 x ld or k < 64 x ld)
       const bf16* base = KC ? op.base + r0 * op.ld + k0 : op.base + k0 * op.ld + r0;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
+      for (int k = 0; k < PERW; ++k) {
         uint32_t o;
         if (KC) {
           o = ((k & 1) ? off1 : off0) + (uint32_t)(16 * (k >> 1) * op.ld);
@@ -93,37 +95,38 @@ struct SlabLoad {
           const int r = wrow + 2 * k + lrow;
           o = (uint32_t)(r * op.ld + 8 * (lpc ^ swz_nkc(r)));
         }
-        __builtin_amdgcn_global_load_lds(base + o, (lds_void*)(lds + (wu * 8 + k) * 512), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(base + o, (lds_void*)(lds + (wu * PERW + k) * 512), 16, 0, 0);
       }
       return;
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < PERW; ++k) {
       const int r = KC ? wrow + 8 * k + lrow : wrow + 2 * k + lrow;
       const int c = KC ? (lpc ^ swz_kc(r)) : (lpc ^ swz_nkc(r));
       int64_t gr = KC ? r0 + r : k0 + r;
       int64_t gc = KC ? k0 + 8 * c : r0 + 8 * c;
       gr = gr < op.rows ? gr : op.rows - 1;
       gc = gc < op.cols ? gc : op.cols - 8;
-      __builtin_amdgcn_global_load_lds(op.base + gr * op.ld + gc, (lds_void*)(lds + (wu * 8 + k) * 512), 16, 0,
-                                       0);
+      __builtin_amdgcn_global_load_lds(op.base + gr * op.ld + gc, (lds_void*)(lds + (wu * PERW + k) * 512), 16,
+                                       0, 0);
     }
   }
 };
 
-// MFMA operand reads of the wave's 128-row block of a slab (4 tiles of 32):
-// returns for lane l the 8 k values (16 ks + 8 h + i, i = 0..7) of operand row
-// 32 t + rowmap(l % 32), with rowmap = perm32 when PERM (A operands: the
-// product's rows then come out as 8 consecutive indices per accumulator
-// group) and the identity otherwise (B operands).
-template <bool KC, bool PERM>
+// MFMA operand reads of the wave's block of NTL 32-row tiles of a slab,
+// starting at slab row (KC) / column (NKC) `base`: returns for lane l the 8 k
+// values (16 ks + 8 h + i, i = 0..7) of operand row base + 32 t +
+// rowmap(l % 32), with rowmap = perm32 when PERM (A operands: the product's
+// rows then come out as 8 consecutive indices per accumulator group) and the
+// identity otherwise (B operands).
+template <bool KC, bool PERM, int NTL>
 struct SlabRead {
   uint32_t off[4][2];  // KC: [ks][-]; NKC: [t][e]
   int rowb;
-  __device__ __forceinline__ void init(int lane, int wblock) {
+  __device__ __forceinline__ void init(int lane, int base) {
     const int l32 = lane & 31, h = lane >> 5;
     if (KC) {
-      const int r = 128 * wblock + (PERM ? perm32(l32) : l32);
+      const int r = base + (PERM ? perm32(l32) : l32);
       const int f = swz_kc(r);
       rowb = r * BK;
 #pragma unroll
@@ -136,8 +139,8 @@ struct SlabRead {
         const int r = 8 * (G >> 1) + j + 4 * e;  // row within a 16-row k group
         const int f = swz_nkc(r);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int col = 128 * wblock + 32 * t + cs;
+        for (int t = 0; t < NTL; ++t) {
+          const int col = base + 32 * t + cs;
           off[t][e] = (uint32_t)(r * 256 + ((((col >> 3) & 15) ^ f) << 3) + ((col >> 7) << 7) + (col & 7));
         }
       }
@@ -165,18 +168,21 @@ struct DzForm {
   int64_t nvt, nc, vocab;
 };
 
+// Each of the 512 threads owns 4 chunks of one token row; the chunk visited at
+// step k is staggered by row so that every quarter-wave touches 16 distinct
+// bank groups.
 template <bool KC>
 __device__ __forceinline__ void dz_pass(const DzForm& F, bf16* S, int64_t j0, int64_t k0, int tid) {
-  int r, c0;
+  int r, q;
   int64_t tok, vbase;
-  if (KC) {  // [256 tok][64 v]: J = tok, k = v
-    r = tid;
-    c0 = 0;
+  if (KC) {  // [256 tok][64 v] (8 chunks / row): J = tok, k = v
+    r = tid >> 1;
+    q = tid & 1;
     tok = j0 + r;
     vbase = k0;
-  } else {   // [64 tok][256 v]: k = tok, J = v
-    r = tid >> 2;
-    c0 = (tid & 3) * 8;
+  } else {   // [64 tok][256 v] (32 chunks / row): k = tok, J = v
+    r = tid >> 3;
+    q = tid & 7;
     tok = k0 + r;
     vbase = j0;
   }
@@ -184,14 +190,14 @@ __device__ __forceinline__ void dz_pass(const DzForm& F, bf16* S, int64_t j0, in
   const int64_t tile = (KC ? k0 : j0) / kVT;
   const float fv = tv ? F.f[tok * F.nvt + tile] : 0.f;
   const float gv = tv ? F.g[tok] : 0.f;
-  // label and vocabulary end relative to this thread's first column (32-bit)
+  // label and vocabulary end relative to this row's first column (32-bit)
   const int64_t yrel64 = tv ? F.y[tok] - vbase : -1;
   const int yrel = (yrel64 >= 0 && yrel64 < 256) ? (int)yrel64 : -1;
   const int64_t vend64 = F.vocab - vbase;
   const int vend = vend64 > 256 ? 256 : (int)vend64;
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int pc = c0 + k;
+  for (int k = 0; k < 4; ++k) {
+    const int pc = KC ? 4 * q + ((k + (r >> 1)) & 3) : 4 * q + ((k + r + 2 * (q >> 2)) & 3);
     const int c = KC ? (pc ^ swz_kc(r)) : (pc ^ swz_nkc(r));
     bf16* ptr = S + (KC ? r * BK : r * 256) + pc * 8;
     const bf16x8 e = ld_bf16x8(ptr);
@@ -211,34 +217,31 @@ __device__ __forceinline__ void dz_pass(const DzForm& F, bf16* S, int64_t j0, in
   }
 }
 
-// Maps a 1-D block id onto (I tile, J tile) so that the blocks sharing the
-// big operand tile run back to back on one XCD (block b is dispatched to XCD
-// b % 8): each XCD gets a contiguous run of the linear tile order, whose
-// fastest dimension is J when JFAST, I otherwise.
-template <bool JFAST>
-__device__ __forceinline__ bool tile_of(int nI, int nJ, int& ti, int& tj) {
+// Maps a 1-D block id onto (I tile, J tile).  Block b is dispatched to XCD
+// b % 8, so each XCD gets a contiguous run of the linear tile order; inside it
+// tiles go in groups of GI I-tiles (I fastest), so the 32 workgroups running
+// together on an XCD cover about GI I-tiles x 32/GI J-tiles and both operands'
+// slabs are shared through that XCD's L2.
+__device__ __forceinline__ bool tile_of(int nI, int nJ, int GI, int& ti, int& tj) {
   const int total = nI * nJ;
   const int per = (total + kXcds - 1) / kXcds;
   const int lin = (int)(blockIdx.x % kXcds) * per + (int)(blockIdx.x / kXcds);
   if (lin >= total) return false;
-  if (JFAST) {
-    ti = lin / nJ;
-    tj = lin % nJ;
-  } else {
-    tj = lin / nI;
-    ti = lin % nI;
-  }
+  const int g = lin / (GI * nJ), within = lin - g * GI * nJ;
+  const int gsize = min(GI, nI - g * GI);
+  ti = g * GI + within % gsize;
+  tj = within / gsize;
   return true;
 }
 
 // C[i][j] = sum_k A[i][k] B[j][k] over k in [kb, ke) (kb, ke multiples of BK
-// except ke at the operand's end) with 4 waves of 128x128 (4x4 MFMA 32x32
-// tiles).  acc[ti][tj][r] holds i = i0 + 128*wi + 32*ti + drow(r, h),
-// j = j0 + 128*wj + 32*tj + l32.  With BFORM the B slab is turned into dZ in
-// LDS after it lands.
+// except ke at the operand's end) with 8 waves of 128x64 (4x2 MFMA 32x32
+// tiles; two waves per SIMD).  acc[ti][tj][r] holds
+// i = i0 + 128*wi + 32*ti + drow(r, h), j = j0 + 64*wj + 32*tj + l32.  With
+// BFORM the B slab is turned into dZ in LDS after it lands.
 template <bool AKC, bool BKC, bool BFORM>
 __device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B, const DzForm& form, int64_t i0,
-                                          int64_t j0, int64_t kb, int64_t ke, f32x16 (&acc)[4][4]) {
+                                          int64_t j0, int64_t kb, int64_t ke, f32x16 (&acc)[4][2]) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wi = w & 1, wj = w >> 1;
   const int wu = __builtin_amdgcn_readfirstlane(w);
@@ -246,14 +249,14 @@ __device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B
   SlabLoad<BKC> lb;
   la.init(A, lane, w);
   lb.init(B, lane, w);
-  SlabRead<AKC, true> ra;
-  SlabRead<BKC, false> rb;
-  ra.init(lane, wi);
-  rb.init(lane, wj);
+  SlabRead<AKC, true, 4> ra;
+  SlabRead<BKC, false, 2> rb;
+  ra.init(lane, 128 * wi);
+  rb.init(lane, 64 * wj);
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) acc[a][b] = zero16();
+    for (int b = 0; b < 2; ++b) acc[a][b] = zero16();
   const int nk = ke > kb ? (int)((ke - kb + BK - 1) / BK) : 0;
   if (nk > 0) {
     la.issue(A, i0, kb, smem, wu);
@@ -277,16 +280,15 @@ __device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B
     }
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 af[4], bfr[4];
+      bf16x8 af[4], bfr[2];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        af[t] = ra.read(As, t, ks);
-        bfr[t] = rb.read(Bs, t, ks);
-      }
+      for (int t = 0; t < 4; ++t) af[t] = ra.read(As, t, ks);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) bfr[t] = rb.read(Bs, t, ks);
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = mfma32(af[a], bfr[b], acc[a][b]);
+        for (int b = 0; b < 2; ++b) acc[a][b] = mfma32(af[a], bfr[b], acc[a][b]);
     }
     wait_vmem();
     __syncthreads();
@@ -309,21 +311,21 @@ struct LogitsArgs {
   int nI, nJ;
 };
 
-__global__ __launch_bounds__(256) void flce_logits_kernel(const LogitsArgs p) {
+__global__ __launch_bounds__(NT) void flce_logits_kernel(const LogitsArgs p) {
   __shared__ __align__(16) bf16 smem[4 * SLAB];
   int ti, tj;
-  if (!tile_of<true>(p.nI, p.nJ, ti, tj)) return;
+  if (!tile_of(p.nI, p.nJ, 4, ti, tj)) return;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
-  f32x16 acc[4][4];
+  f32x16 acc[4][2];
   DzForm none{};
   gemm_core<true, true, false>(smem, p.W, p.H, none, i0, j0, 0, p.W.cols, acc);
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int wi = w & 1, wj = w >> 1;
   float* red = reinterpret_cast<float*>(smem);  // [2][256]
-  float mt[4];
+  float mt[2];
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
+  for (int b = 0; b < 2; ++b) {
     float mx = -INFINITY;
 #pragma unroll
     for (int a = 0; a < 4; ++a)
@@ -335,18 +337,18 @@ __global__ __launch_bounds__(256) void flce_logits_kernel(const LogitsArgs p) {
         mx = fmaxf(mx, z2);
       }
     mx = wave_max_xor32(mx);
-    if (h == 0) red[wi * 256 + 128 * wj + 32 * b + l32] = mx;
+    if (h == 0) red[wi * 256 + 64 * wj + 32 * b + l32] = mx;
   }
   __syncthreads();
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int col = 128 * wj + 32 * b + l32;
+  for (int b = 0; b < 2; ++b) {
+    const int col = 64 * wj + 32 * b + l32;
     mt[b] = fmaxf(red[col], red[256 + col]);
   }
   __syncthreads();
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int col = 128 * wj + 32 * b + l32;
+  for (int b = 0; b < 2; ++b) {
+    const int col = 64 * wj + 32 * b + l32;
     const int64_t tok = j0 + col;
     const bool tv = tok < p.nc;
     const int64_t yv = tv ? p.y[tok] : -1;
@@ -374,8 +376,8 @@ __global__ __launch_bounds__(256) void flce_logits_kernel(const LogitsArgs p) {
   __syncthreads();
   if (wi == 0 && h == 0) {
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int col = 128 * wj + 32 * b + l32;
+    for (int b = 0; b < 2; ++b) {
+      const int col = 64 * wj + 32 * b + l32;
       const int64_t tok = j0 + col;
       if (tok < p.nc) {
         p.mpart[tok * p.nvt + ti] = mt[b];
@@ -433,21 +435,21 @@ struct DhArgs {
   int nI, nJ, splits;
 };
 
-__global__ __launch_bounds__(256) void flce_dh_kernel(const DhArgs p) {
+__global__ __launch_bounds__(NT) void flce_dh_kernel(const DhArgs p) {
   __shared__ __align__(16) bf16 smem[4 * SLAB];
   int ti, tj;
-  if (!tile_of<false>(p.nI, p.nJ, ti, tj)) return;
+  if (!tile_of(p.nI, p.nJ, p.nI, ti, tj)) return;
   const int split = blockIdx.y;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
   const int64_t kb = split * p.kper;
   const int64_t ke = min(p.E.cols, kb + p.kper);
-  f32x16 acc[4][4];
+  f32x16 acc[4][2];
   gemm_core<false, true, true>(smem, p.Wt, p.E, p.form, i0, j0, kb, ke, acc);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int wi = w & 1, wj = w >> 1;
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int64_t tok = j0 + 128 * wj + 32 * b + l32;
+  for (int b = 0; b < 2; ++b) {
+    const int64_t tok = j0 + 64 * wj + 32 * b + l32;
     if (tok >= p.nc) continue;
 #pragma unroll
     for (int a = 0; a < 4; ++a)
@@ -507,18 +509,18 @@ struct DwArgs {
   int mode;      // 0: bf16 store; 1: fp32 store; 2: fp32 add; 3: fp32 add + bf16 store
 };
 
-__global__ __launch_bounds__(256) void flce_dw_kernel(const DwArgs p) {
+__global__ __launch_bounds__(NT) void flce_dw_kernel(const DwArgs p) {
   __shared__ __align__(16) bf16 smem[4 * SLAB];
   int ti, tj;
-  if (!tile_of<false>(p.nI, p.nJ, ti, tj)) return;
+  if (!tile_of(p.nI, p.nJ, p.nI, ti, tj)) return;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
-  f32x16 acc[4][4];
+  f32x16 acc[4][2];
   gemm_core<false, false, true>(smem, p.Ht, p.Et, p.form, i0, j0, 0, p.Ht.rows, acc);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int wi = w & 1, wj = w >> 1;
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int64_t v = j0 + 128 * wj + 32 * b + l32;
+  for (int b = 0; b < 2; ++b) {
+    const int64_t v = j0 + 64 * wj + 32 * b + l32;
     if (v >= p.V) continue;
 #pragma unroll
     for (int a = 0; a < 4; ++a)
