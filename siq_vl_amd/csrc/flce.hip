@@ -50,10 +50,11 @@ struct GOp {
 //    of 16 consecutive rows per quarter-wave): swz_kc spreads 16 rows over
 //    distinct (bank half, chunk) pairs.
 //  * NKC: [64 k][256 cols], 512-byte rows; the slab's columns are the operand's
-//    M (or N) index.  Read with ds_read_b64_tr_b16 (a chunk pair from each of 4
-//    consecutive rows per quarter-wave): swz_nkc makes the 4 pairs disjoint.
+//    M (or N) index.  Read with ds_read_b64_tr_b16 (4 aligned chunks from each
+//    of 4 consecutive rows per half-wave): swz_nkc XORs the row into bits 2-3
+//    of the chunk index, so the 16 positions land in 16 distinct bank groups.
 __device__ __forceinline__ int swz_kc(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
-__device__ __forceinline__ int swz_nkc(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+__device__ __forceinline__ int swz_nkc(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 // Direct global->LDS staging of one slab: 32 instructions of 1 KB, 8 per wave.
 // Rows / chunks past the operand's extent re-read the last valid one (always in

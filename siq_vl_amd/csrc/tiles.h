@@ -13,9 +13,11 @@
 //  * row operand (ds_read_b128): a quarter-wave reads one chunk from each of
 //    16 consecutive rows -> swz must be a bijection on (r mod 16) for D = 128
 //    (a 256-byte row spans all banks) and on (r mod 2, chunk) for D = 64;
-//  * transposed operand (ds_read_b64_tr_b16): a quarter-wave reads the chunk
-//    pair (2a, 2a + 1) of 4 consecutive rows -> the 4 pairs must be disjoint.
-// D = 128: swz(r) = 2 (r mod 8) + bit3(r);  D = 64: swz(r) = 2 (bits 1-2 of r) + bit3(r).
+//  * transposed operand (ds_read_b64_tr_b16): half a wave reads the 4 chunks
+//    c0 .. c0 + 3 (c0 a multiple of 4) of 4 consecutive rows (first row a
+//    multiple of 4) -> the 16 chunk positions must fall in distinct bank groups.
+// D = 128: swz(r) = 4 (r mod 4) + (r / 4 mod 4)   (bits 2-3 separate the rows)
+// D = 64:  swz(r) = 4 (r / 2 mod 2) + (r / 4 mod 4) (rows alternate bank halves)
 #pragma once
 #include "common.h"
 
@@ -27,8 +29,8 @@ typedef __attribute__((address_space(3))) void lds_void;
 template <int D>
 __device__ __forceinline__ int swz(int r) {
   static_assert(D == 128 || D == 64, "head dim");
-  if (D == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
-  return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
+  if (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
 }
 
 __device__ __forceinline__ int wave_uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
