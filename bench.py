@@ -35,6 +35,7 @@ from siq_vl_amd import workloads as W
 
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CUs x 2.4 GHz)
 PEAK_HBM_GBS = 8000.0
+COPY_BYTES = 256 << 20
 METRIC = "packed varlen attn fwd+bwd TFLOP/s (% bf16 MFMA peak); fused-CE tokens/s"
 
 
@@ -131,7 +132,9 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
     """Reference path (oracle/cpu_path.py) on the host cores, bounded sample."""
     from oracle import cpu_path
 
-    threads = os.cpu_count() or 1
+    # the host share this GPU's job may use (OMP_NUM_THREADS on the GPU box), never above the core count
+    cores = os.cpu_count() or 1
+    threads = min(cores, int(os.environ.get("OMP_NUM_THREADS") or cores))
     torch.set_num_threads(threads)
     res = {}
     # attention: the first sequences of the config-2 batch, ~2048 tokens
@@ -192,6 +195,9 @@ def main() -> int:
     ap.add_argument("--ce-chunk", type=int, default=C.DEFAULT_CHUNK_TOKENS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-ce", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy (3 times): the known-size reference that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
@@ -200,6 +206,15 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+
+    if args.calibrate_copy:
+        src = torch.ones(COPY_BYTES, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] copied {COPY_BYTES} bytes 3 times", file=sys.stderr, flush=True)
+        return 0
 
     att = bench_attention(args.steps, args.warmup)
     print(f"[bench] attention fwd+bwd {att['ms_per_step']:.3f} ms/step, {att['tflops']:.1f} TFLOP/s "

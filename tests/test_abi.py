@@ -1,0 +1,168 @@
+"""The C ABI of libsiq_kernels.so, exercised on the CPU: every symbol the
+header declares is exported, and host-side validation rejects bad arguments
+with the documented status before anything reaches the GPU."""
+
+import re
+from pathlib import Path
+
+import pytest
+
+from siq_vl_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "siq_kernels.h"
+FAKE = 0x10000  # 16-byte aligned, never dereferenced: validation fails first
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(siq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_symbols():
+    assert declared_symbols() == sorted(_lib.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    m = re.search(r"#define\s+SIQ_ABI_VERSION\s+(\d+)", HEADER.read_text())
+    assert m and lib.siq_abi_version() == int(m.group(1))
+
+
+def test_status_codes_match_header():
+    text = HEADER.read_text()
+    for name in ("SIQ_OK", "SIQ_ERR_INVALID_ARGUMENT", "SIQ_ERR_UNSUPPORTED", "SIQ_ERR_WORKSPACE",
+                 "SIQ_ERR_ALIGNMENT", "SIQ_ERR_LAUNCH"):
+        m = re.search(name + r"\s*=\s*(-?\d+)", text)
+        assert m, name
+        assert int(m.group(1)) == getattr(_lib, name)
+
+
+def test_workspace_sizes(lib):
+    f = lib.siq_attn_fwd_workspace_bytes
+    b = lib.siq_attn_bwd_workspace_bytes
+    assert f(-1, 10, 10, 2, 1, 64) == 0 and b(2, 10, 10, 0, 1, 64) == 0
+    small, big = f(4, 1000, 1000, 12, 2, 128), f(64, 100000, 100000, 12, 2, 128)
+    assert 0 < small < big
+    assert b(4, 1000, 1000, 12, 2, 128) > f(4, 1000, 1000, 12, 2, 128)  # bwd adds Delta
+    assert f(4, 1000, 1000, 12, 2, 128) % 16 == 0
+    w = lib.siq_flce_workspace_bytes
+    assert w(-1, 64, 64, 8, 1) == 0
+    a, c = w(16384, 1536, 151936, 8192, 1), w(16384, 1536, 151936, 2048, 1)
+    assert a > c > 0  # chunk bounds the logits-sized scratch
+    # never a full [n, V] fp32 logits buffer
+    assert a < 16384 * 151936 * 4
+
+
+def _strides(n=16):
+    return _lib.int64_array([128] * n)
+
+
+def _attn_fwd(lib, **kw):
+    args = dict(q=FAKE, k=FAKE, v=FAKE, o=FAKE, lse=FAKE, cu_q=FAKE, cu_k=FAKE, batch=2, max_q=8, max_k=8,
+                total_q=16, total_k=16, hq=4, hkv=2, d=128, strides=_strides(8), scale=0.1, causal=1, ws=None,
+                ws_bytes=0, stream=None)
+    args.update(kw)
+    return lib.siq_attn_varlen_fwd(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(d=96), _lib.SIQ_ERR_UNSUPPORTED),
+    (dict(hq=3), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(hkv=0), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(batch=-1), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(total_q=1 << 31), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(scale=float("nan")), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(cu_q=None), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(strides=None), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(q=FAKE + 8), _lib.SIQ_ERR_ALIGNMENT),
+    (dict(v=None), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(lse=FAKE + 2), _lib.SIQ_ERR_ALIGNMENT),
+    (dict(ws=None), _lib.SIQ_ERR_WORKSPACE),
+    (dict(ws=FAKE, ws_bytes=16), _lib.SIQ_ERR_WORKSPACE),
+])
+def test_attention_fwd_validation(lib, kw, code):
+    assert _attn_fwd(lib, **kw) == code
+    assert lib.siq_last_error().decode()
+
+
+def test_attention_fwd_odd_strides_rejected(lib):
+    st = _lib.int64_array([128, 128, 130, 128, 128, 128, 128, 128])
+    assert _attn_fwd(lib, strides=st) == _lib.SIQ_ERR_ALIGNMENT
+
+
+def test_attention_empty_batch_is_a_no_op(lib):
+    # nothing to compute: returns before touching the device
+    assert _attn_fwd(lib, batch=0, total_q=0, total_k=0, q=None, k=None, v=None, o=None, lse=None) == _lib.SIQ_OK
+
+
+def test_attention_bwd_validation(lib):
+    rc = lib.siq_attn_varlen_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 8, 16, 16,
+                                 4, 2, 64, _strides(16), 0.1, 1, FAKE, 8, None)
+    assert rc == _lib.SIQ_ERR_WORKSPACE
+    rc = lib.siq_attn_varlen_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, FAKE, 2, 8, 8, 16, 16,
+                                 4, 2, 64, _strides(16), 0.1, 1, None, 0, None)
+    assert rc == _lib.SIQ_ERR_INVALID_ARGUMENT and b"dq" in lib.siq_last_error()
+
+
+def _flce(lib, **kw):
+    args = dict(hidden=FAKE, weight=FAKE, labels=FAKE, n=16, hdim=128, vocab=1024, ignore_index=-100, reduction=0,
+                divisor=None, loss=FAKE, count=FAKE, bad=FAKE, dh=FAKE, dw=FAKE, chunk=8, ws=None, ws_bytes=0,
+                stream=None)
+    args.update(kw)
+    return lib.siq_flce_fwd_bwd(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(hdim=100), _lib.SIQ_ERR_UNSUPPORTED),
+    (dict(vocab=1001), _lib.SIQ_ERR_UNSUPPORTED),
+    (dict(n=-1), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(reduction=2), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(reduction=1), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(loss=None), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(labels=None), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(hidden=FAKE + 4), _lib.SIQ_ERR_ALIGNMENT),
+    (dict(weight=None), _lib.SIQ_ERR_ALIGNMENT),
+    (dict(chunk=0), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(ws=FAKE, ws_bytes=64), _lib.SIQ_ERR_WORKSPACE),
+])
+def test_flce_validation(lib, kw, code):
+    assert _flce(lib, **kw) == code
+    assert lib.siq_last_error().decode()
+
+
+def test_scale_validation(lib):
+    assert lib.siq_scale_bf16_inplace(None, 0, None, None) == _lib.SIQ_OK
+    assert lib.siq_scale_bf16_inplace(None, -1, None, None) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    assert lib.siq_scale_bf16_inplace(FAKE + 2, 8, FAKE, None) == _lib.SIQ_ERR_ALIGNMENT
+
+
+def test_check_maps_status_to_exceptions():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.SIQ_ERR_INVALID_ARGUMENT, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.SIQ_ERR_LAUNCH, "x")
+    _lib.check(_lib.SIQ_OK, "x")
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setenv("SIQ_KERNELS_LIB", str(tmp_path / "absent.so"))
+    with pytest.raises(RuntimeError, match="build"):
+        _lib.lib()
+
+
+def test_ctypes_prototypes_cover_header_arity():
+    """Each bound prototype has the parameter count of its header declaration."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    for name, (_, args) in _lib._PROTOS.items():
+        m = re.search(r"\b" + name + r"\s*\(([^)]*)\)", text)
+        assert m, name
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(args), (name, len(params), len(args))
