@@ -36,6 +36,17 @@ from siq_vl_amd import workloads as W
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CUs x 2.4 GHz)
 PEAK_HBM_GBS = 8000.0
 COPY_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+
+
+def measured_traffic(key: str):
+    """HBM bytes per call of ``key`` from the last rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes (scaled by a plain copy's readings), or None if never measured."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            return int(json.load(fh)[key]["bytes_per_call"])
+    except (OSError, KeyError, ValueError):
+        return None
 METRIC = "packed varlen attn fwd+bwd TFLOP/s (% bf16 MFMA peak); fused-CE tokens/s"
 
 
@@ -94,6 +105,7 @@ def bench_attention(steps: int, warmup: int) -> dict:
         "bwd_tflops": flops_bwd / (med(bwd_ms) * 1e-3) / 1e12,
         "flops_bwd": flops_bwd,
         "bytes": bytes_fwd + bytes_bwd,
+        "bytes_bwd": bytes_bwd,
         "pairs": pairs,
     }
 
@@ -249,7 +261,9 @@ def main() -> int:
                    "fwd_tflops": round(att["fwd_tflops"], 2), "bwd_tflops": round(att["bwd_tflops"], 2)},
         "roofline": {"bound": "mfma", "kernel": "attention backward call (preprocess + dK/dV + dQ kernels)",
                      "achieved": round(bwd_achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(bwd_achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(bwd_achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic("attention_bwd_config2"),
+                     "algorithmic_bytes": att["bytes_bwd"]},
         "cpu_baseline": cpu["attn"] if cpu else None,
     }
     if ce is not None:
