@@ -10,9 +10,44 @@ namespace siq {
 // Tile sizes shared by the scheduler and the kernels.
 constexpr int kFwdBM = 128;    // q rows per forward / dQ workgroup (4 waves x 32)
 constexpr int kFwdBN = 64;     // kv rows per inner step of the forward / dQ loop
-constexpr int kBwdBN = 32;     // kv rows per dK/dV workgroup (shared by its 4 waves)
-constexpr int kBwdBM = 128;    // q rows per inner step of the dK/dV loop (4 waves x 32)
+constexpr int kBwdBN = 128;    // kv rows per dK/dV work item (4 quarters of 32)
+constexpr int kBwdBM = 64;     // q rows per step of the dK/dV loop (2 groups of 32)
 constexpr int kSchedKeys = 2048;
+// dK/dV load balance: a kv tile's steps (q block x q-head of the GQA group) run
+// in one workgroup unless the tile is heavier than total / kSplitTarget steps;
+// heavier tiles are cut into pieces whose fp32 partial sums are added, in
+// piece order, by a small kernel after the dK/dV kernel.
+constexpr int kSplitTarget = 384;
+constexpr int kMinSplitSteps = 4;
+constexpr int kSplitSlots = 2 * kSplitTarget + 2;  // bound on sum(pieces x hkv) over split tiles
+constexpr int kMaxSplitTiles = kSplitSlots / 2;    // a split tile has >= 2 pieces
+constexpr int kXcds = 8;                           // MI355X: workgroup b runs on XCD b % 8
+constexpr int kWorkBucketsMax = 16;                // scheduler scratch: work classes x batch ints
+
+// One dK/dV work item: steps [s0, s1) of kv tile t of sequence b; piece `piece`
+// of np (np == 1: the whole tile, written directly as bf16).  Steps walk the
+// q blocks downwards from the last one, each over the n_rep q-heads, so the
+// tiles of one sequence read the same Q / dO block at the same step.  A piece
+// of a split tile writes fp32 sums to slot (slot0 + piece) * hkv + hk.
+struct KvItem {
+  int b, t, s0, s1, piece, np, slot0, pad;
+};
+// A split tile, for the kernel that adds its pieces' partial sums.
+struct SplitTile {
+  int b, t, np, slot0;
+};
+
+// Block b of a launch runs on XCD b % 8.  Hands each XCD runs of G consecutive
+// entries of a work list (a bijection on [0, n)), so that the workgroups
+// resident on one XCD at the same time work on neighbouring entries and share
+// their operands through that XCD's L2.  Entries past the last whole run of
+// 8 G keep their index.
+__device__ __forceinline__ int xcd_order(int b, int n, int G) {
+  const int full = (n / (kXcds * G)) * (kXcds * G);
+  if (b >= full) return b;
+  const int x = b % kXcds, k = b / kXcds;  // k-th block dispatched to XCD x
+  return ((k / G) * kXcds + x) * G + (k % G);
+}
 
 struct AttnParams {
   const bf16* q;
@@ -26,9 +61,13 @@ struct AttnParams {
   bf16* dk;
   bf16* dv;
   float* delta;      // [hq, lse_head] rowsum(dO * O) (backward workspace)
+  float* lse2;       // [hq, lse_head] LSE * log2(e) (backward workspace)
   const SeqInfo* seq;
   const int2* qtiles;   // (sequence, q-tile) ordered by decreasing work; x < 0 = idle
-  const int2* kvtiles;  // (sequence, kv-tile) for the dK/dV kernel
+  const KvItem* kvitems;     // dK/dV work items (longest sequences first); b < 0 = idle
+  float* dkv_part;           // [kSplitSlots][2][kBwdBN][D] fp32 partial dK / dV of split tiles
+  const SplitTile* splits;   // [kMaxSplitTiles] split tiles
+  const int* nsplit;         // number of split tiles
   int batch, hq, hkv, n_rep;
   int64_t q_tok, q_head, k_tok, k_head, v_tok, v_head, o_tok, o_head;
   int64_t do_tok, do_head, dq_tok, dq_head, dk_tok, dk_head, dv_tok, dv_head;
@@ -41,10 +80,12 @@ struct AttnParams {
 // Upper bound on the number of tiles of `rows` rows over `batch` sequences
 // holding `total` tokens: sum ceil(L_b / rows) <= total / rows + batch.
 inline int64_t tile_cap(int64_t total, int batch, int rows) { return total / rows + batch + 1; }
+// Upper bound on the number of dK/dV work items (tiles plus extra pieces).
+inline int64_t kv_item_cap(int64_t total_k, int batch) { return tile_cap(total_k, batch, kBwdBN) + kSplitTarget + 1; }
 
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,
-                           int causal, SeqInfo* seq, int2* qtiles, int qcap, int2* kvtiles, int kvcap,
-                           hipStream_t stream);
+                           int causal, int n_rep, int hkv, SeqInfo* seq, int2* qtiles, int qcap, KvItem* kvitems,
+                           int kvcap, int* seqbuf, SplitTile* splits, int* nsplit, hipStream_t stream);
 hipError_t launch_attn_fwd(const AttnParams& p, int d, int causal, int qcap, hipStream_t stream);
 hipError_t launch_attn_bwd(const AttnParams& p, int d, int causal, int qcap, int kvcap, hipStream_t stream);
 

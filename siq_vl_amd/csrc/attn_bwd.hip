@@ -9,13 +9,18 @@
 //
 // Three kernels:
 //  * preprocess: Delta = rowsum(dO o O)                      (HBM-bound)
-//  * dK/dV: one workgroup = 32 kv rows of one kv-head.  K and V of those rows
-//    sit in every wave's registers as B operands of S = Q K^T and dP = dO V^T
-//    (lane = kv column).  The workgroup walks every q-head of the GQA group and
-//    every q block that can see the rows, 128 q rows per step (32 per wave),
-//    with Q and dO tiles staged in LDS by direct global->LDS loads; dV^T +=
-//    dO^T P and dK^T += Q^T dS read dO^T / Q^T with ds_read_b64_tr_b16.  The four waves'
-//    partial dK/dV are summed through LDS at the end and written once.
+//  * dK/dV: one workgroup = 8 waves = 128 kv rows of one kv-head.  Wave
+//    (g, kq) owns kv rows 32 kq .. 32 kq + 31 and q rows 32 g .. 32 g + 31 of
+//    each 64-row step, so every staged Q / dO tile feeds all 128 kv rows and
+//    every SIMD runs two waves.  K of the wave's rows sits in registers as the
+//    B operand of S = Q K^T, V in LDS as the B operand of dP = dO V^T.  A work
+//    item walks steps (q-head of the GQA group, q block) of its kv tile, with
+//    Q / dO / LSE2 / Delta triple-buffered in LDS by direct global->LDS loads
+//    (two steps in flight); dV^T += dO^T P and dK^T += Q^T dS read dO^T / Q^T
+//    with ds_read_b64_tr_b16.  The two q-group waves' partial dK/dV of each kv
+//    quarter are summed through LDS.  Tiles heavier than the scheduler's
+//    piece length run as several work items writing fp32 sums to workspace
+//    slots, which a small kernel adds in piece order afterwards.
 //  * dQ: one workgroup = 128 q rows of one q-head (same schedule as the
 //    forward); Q and dO in registers as B operands of S^T = K Q^T and
 //    dP^T = V dO^T, K and V tiles row-major in LDS, dQ^T += K^T dS^T with K^T
@@ -42,186 +47,262 @@ __global__ __launch_bounds__(256) void attn_bwd_preprocess_kernel(const AttnPara
     for (int i = 0; i < 8; ++i) acc += (float)o[i] * (float)g[i];
 #pragma unroll
     for (int m = TPR / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
-    if (sub == 0) p.delta[(int64_t)hh * p.lse_head + t] = acc;
+    if (sub == 0) {
+      const int64_t idx = (int64_t)hh * p.lse_head + t;
+      p.delta[idx] = acc;
+      p.lse2[idx] = p.lse[idx] * kLog2e;
+    }
   }
 }
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnParams p) {
-  constexpr int BN = kBwdBN, BM = kBwdBM, NT = 256;
-  static_assert(BN == 32 && BM == 128, "one 32-row kv tile, 32 q rows per wave");
-  using QTile = LdsTile<BM, D, NT / 64>;
+__global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams p) {
+  constexpr int BN = kBwdBN, BM = kBwdBM, NT = 512, NW = NT / 64, NS = 2;
+  static_assert(BN == 128 && BM == 64, "128 kv rows (4 x 32) by 64 q rows (2 x 32) per step");
+  using QTile = LdsTile<BM, D, NW / 2>;  // Q staged by waves 0-3, dO by waves 4-7
+  using KVTile = LdsTile<BN, D, NW>;
   constexpr int TE = QTile::ELEMS;
   constexpr int STAGE = 2 * TE;  // Q, dO (bf16 elements)
-  __shared__ __align__(16) bf16 smem[2 * STAGE];
-  __shared__ __align__(16) float rowv[2][2][BM];  // [stage][lse | delta][q] (raw, as loaded)
+  constexpr int NDT = D / 32;
+  constexpr int SMEM = NS * STAGE + 2 * KVTile::ELEMS;  // stages, K, V
+  static_assert(2 * 4 * NDT * 16 * 64 * 4 <= SMEM * 2, "one reduction round fits the LDS");
+  __shared__ __align__(16) bf16 smem[SMEM];
+  __shared__ __align__(16) float rowv[NS][2][BM];  // [stage][lse2 | delta][q] (raw, as loaded)
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
-  const int wu = wave_uniform(w);
-  QTile qt, gt;
-  qt.init(p.q_tok, lane);
-  gt.init(p.do_tok, lane);
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int wu = wave_uniform(tid >> 6);
+  const int g = wu & 1, kq = wu >> 1;     // q group (32 rows of a step), kv quarter (32 rows of the tile)
+  const bool stages_q = wu < 4;           // waves 0-3 stage Q, waves 4-7 stage dO
+  const bool stages_row = (wu & 3) == 0;  // waves 0 / 4 also stage the step's LSE2 / Delta
+  QTile st;
+  st.init(stages_q ? p.q_tok : p.do_tok, lane);
+  KVTile kt, vt;
+  kt.init(p.k_tok, lane);
+  vt.init(p.v_tok, lane);
   RowRead<D> rr;
   rr.init(lane);
   TrRead<D> tr;
   tr.init(lane);
   const float c = p.scale_log2;
+  bf16* Ks = smem + NS * STAGE;
+  bf16* Vs = Ks + KVTile::ELEMS;
 
-  const int2 tl = p.kvtiles[blockIdx.x];
-  if (tl.x < 0) return;
-  const SeqInfo si = p.seq[tl.x];
-  const int hk = blockIdx.y;
-  const int k0 = tl.y * BN;
+  // 1-D grid over (item, kv-head), kv-head fastest, runs of 32 per XCD
+  const int e = xcd_order(blockIdx.x, gridDim.x, 32);
+  const int ii = e / p.hkv, hk = e - ii * p.hkv;
+  const KvItem it = p.kvitems[ii];
+  if (it.b < 0) return;
+  const SeqInfo si = p.seq[it.b];
+  const int k0 = it.t * BN;
+  const int kb = k0 + 32 * kq;  // first kv row of this wave
   const int off = si.k_len - si.q_len;
 
-  const int kvrow = k0 + l32;
+  const int kvrow = kb + l32;
   const bool kvvalid = kvrow < si.k_len;
-  bf16x8 kf[D / 16], vf[D / 16];
-  {
-    const int64_t r = si.k_start + (kvvalid ? kvrow : 0);
-    const bf16* kp = p.k + r * p.k_tok + (int64_t)hk * p.k_head + 8 * h;
-    const bf16* vp = p.v + r * p.v_tok + (int64_t)hk * p.v_head + 8 * h;
+  // K and V of the tile in LDS (rows past the end repeat the last row: they
+  // only reach dK / dV rows that are never written)
+  kt.issue(p.k + (int64_t)(si.k_start + k0) * p.k_tok + (int64_t)hk * p.k_head, p.k_tok, si.k_len - k0, Ks, wu);
+  vt.issue(p.v + (int64_t)(si.k_start + k0) * p.v_tok + (int64_t)hk * p.v_head, p.v_tok, si.k_len - k0, Vs, wu);
+  f32x16 dk[NDT], dv[NDT];
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-      const bf16x8 a = ld_bf16x8(kp + 16 * ks), b = ld_bf16x8(vp + 16 * ks);
-      kf[ks] = kvvalid ? a : zero_bf16x8();
-      vf[ks] = kvvalid ? b : zero_bf16x8();
-    }
-  }
-  f32x16 dk[D / 32], dv[D / 32];
-#pragma unroll
-  for (int i = 0; i < D / 32; ++i) {
+  for (int i = 0; i < NDT; ++i) {
     dk[i] = zero16();
     dv[i] = zero16();
   }
 
-  // q blocks that can see any of this tile's kv rows
-  int qb0 = 0;
-  if (CAUSAL) qb0 = max(0, k0 - off) / BM;
-  const int nqb = si.q_len > qb0 * BM ? (si.q_len - qb0 * BM + BM - 1) / BM : 0;
-  const int nsteps = (k0 < si.k_len) ? nqb * p.n_rep : 0;
+  // The tile's steps are (q block qb, q-head j of the GQA group) for the q
+  // blocks that can see any of its rows, q blocks from the last one down, the
+  // n_rep heads inside; this item runs steps [s0, s1).
+  const int qb_last = (si.q_len - 1) / BM;
+  const int s0 = it.s0, ns = it.s1 - it.s0;
 
-  // Stage step `step` into buffer `buf`: Q and dO tiles, plus the 128 LSE and
-  // Delta values (one 64-lane dword direct load per wave; rows past the end
-  // read the last valid row and are fixed at use).
   auto issue = [&](int step, int buf) {
-    const int j = step / nqb, qb = qb0 + step - j * nqb;
+    const int j = step % p.n_rep, qb = qb_last - step / p.n_rep;
     const int hq = hk * p.n_rep + j;
     const int q0 = qb * BM;
     const int nrows = si.q_len - q0;
     const int64_t r0 = si.q_start + q0;
-    bf16* base = smem + buf * STAGE;
-    qt.issue(p.q + r0 * p.q_tok + (int64_t)hq * p.q_head, p.q_tok, nrows, base, wu);
-    gt.issue(p.dout + r0 * p.do_tok + (int64_t)hq * p.do_head, p.do_tok, nrows, base + TE, wu);
-    const int which = wu >> 1, half = wu & 1;
-    const int r = min(64 * half + lane, nrows - 1);
-    const float* src = (which == 0 ? p.lse : p.delta) + (int64_t)hq * p.lse_head + r0 + r;
-    __builtin_amdgcn_global_load_lds(src, (lds_void*)(&rowv[buf][which][64 * half]), 4, 0, 0);
+    const bf16* src = stages_q ? p.q + r0 * p.q_tok + (int64_t)hq * p.q_head
+                               : p.dout + r0 * p.do_tok + (int64_t)hq * p.do_head;
+    st.issue(src, stages_q ? p.q_tok : p.do_tok, nrows, smem + buf * STAGE + (stages_q ? 0 : TE), wu & 3);
+    if (stages_row) {
+      const uint32_t r = (uint32_t)min(lane, nrows - 1);
+      const float* rs = (stages_q ? p.lse2 : p.delta) + (int64_t)hq * p.lse_head + r0;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(rs) + (r << 2),
+                                       (lds_void*)(&rowv[buf][stages_q ? 0 : 1][0]), 4, 0, 0);
+    }
   };
 
-  if (nsteps > 0) issue(0, 0);
+  if (ns > 0) issue(s0, 0);
   wait_vmem();
   __syncthreads();
 
-  for (int step = 0; step < nsteps; ++step) {
-    const int buf = step & 1;
+  for (int i = 0; i < ns; ++i) {
+    const int step = s0 + i;
+    const int buf = i % NS;
     const bf16* Qs = smem + buf * STAGE;
     const bf16* Gs = Qs + TE;
-    const float* lse = rowv[buf][0];
+    const float* lse2 = rowv[buf][0];
     const float* dlt = rowv[buf][1];
-    const int q0 = (qb0 + step % nqb) * BM;
+    const int q0 = (qb_last - step / p.n_rep) * BM;
     const int qvalid = si.q_len - q0;  // rows of this block that exist
-    const bool tail = qvalid < BM;
-    const bool more = step + 1 < nsteps;
-    if (more) issue(step + 1, buf ^ 1);
+    if (i + 1 < ns) issue(step + 1, buf ^ 1);
 
-    const int wq0 = q0 + 32 * w;  // first q row of this wave
-    const bool active = !CAUSAL || (wq0 + 31 + off >= k0);
+    const int wq0 = q0 + 32 * g;  // first q row of this wave
+    const bool active = 32 * g < qvalid && (!CAUSAL || wq0 + 31 + off >= kb);
     if (active) {
-      const bool need_mask = CAUSAL && (wq0 + off < k0 + 31);
-      // accumulator r (= 8j + i) holds q = wq0 + 16j + krow(i, h), kv = kvrow
+      // accumulator r (= 8j + i) holds q = wq0 + 16j + 8(i / 4) + 4h + i % 4, kv = kvrow
+      // operand fragments double-buffered one k-step ahead of the MFMAs
       f32x16 s = zero16(), dp = zero16();
+      bf16x8 fq[2], fg[2], fk[2], fv[2];
+      fq[0] = rr.read(Qs, 32 * g, 0);
+      fk[0] = rr.read(Ks, 32 * kq, 0);
+      fg[0] = rr.read(Gs, 32 * g, 0);
+      fv[0] = rr.read(Vs, 32 * kq, 0);
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
-        s = mfma32(rr.read(Qs, 32 * w, ks), kf[ks], s);
-        dp = mfma32(rr.read(Gs, 32 * w, ks), vf[ks], dp);
+        const int cur = ks & 1;
+        if (ks + 1 < D / 16) {
+          fq[cur ^ 1] = rr.read(Qs, 32 * g, ks + 1);
+          fk[cur ^ 1] = rr.read(Ks, 32 * kq, ks + 1);
+          fg[cur ^ 1] = rr.read(Gs, 32 * g, ks + 1);
+          fv[cur ^ 1] = rr.read(Vs, 32 * kq, ks + 1);
+        }
+        s = mfma32(fq[cur], fk[cur], s);
+        dp = mfma32(fg[cur], fv[cur], dp);
       }
-      const int rel = kvrow - off - wq0 - 4 * h;  // causal: keep q offsets >= rel
-      bf16x8 pb[2], db[2];
+      // P = exp2(S scale log2e - LSE2), dS = P (dP - Delta), in place; on the
+      // causal diagonal and past the end of the sequence the exponent is -inf
+      // (P = 0, hence dS = 0)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int qo = 32 * w + 16 * j + 4 * h;  // krow(i, h) = 4h + i (i < 4), 8 + 4h + i - 4
-        const f32x4 l0 = *reinterpret_cast<const f32x4*>(lse + qo);
-        const f32x4 l1 = *reinterpret_cast<const f32x4*>(lse + qo + 8);
+        const int qo = 32 * g + 16 * j + 4 * h;
+        const f32x4 l0 = *reinterpret_cast<const f32x4*>(lse2 + qo);
+        const f32x4 l1 = *reinterpret_cast<const f32x4*>(lse2 + qo + 8);
         const f32x4 d0 = *reinterpret_cast<const f32x4*>(dlt + qo);
         const f32x4 d1 = *reinterpret_cast<const f32x4*>(dlt + qo + 8);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float lv = (i < 4 ? l0[i] : l1[i - 4]) * kLog2e;
-          float dv_ = i < 4 ? d0[i] : d1[i - 4];
-          if (tail) {  // rows past the end of the sequence: P = exp2(-inf) = 0, Delta = 0
-            const bool ok = qo + 8 * (i >> 2) + (i & 3) < qvalid;
-            lv = ok ? lv : INFINITY;
-            dv_ = ok ? dv_ : 0.f;
-          }
-          float pv = exp2f_fast(__builtin_fmaf(s[8 * j + i], c, -lv));
-          if (need_mask) pv = (16 * j + 8 * (i >> 2) + (i & 3) < rel) ? 0.f : pv;
-          s[8 * j + i] = pv;
-          dp[8 * j + i] = pv * (dp[8 * j + i] - dv_);
+        for (int e = 0; e < 8; ++e) {
+          s[8 * j + e] = __builtin_fmaf(s[8 * j + e], c, -(e < 4 ? l0[e] : l1[e - 4]));
+          dp[8 * j + e] -= e < 4 ? d0[e] : d1[e - 4];
         }
-        pb[j] = pack8(s, 8 * j);
-        db[j] = pack8(dp, 8 * j);
       }
+      if (32 * g + 32 > qvalid || (CAUSAL && wq0 + off < kb + 31)) {
+        const int rel = CAUSAL ? kvrow - off - wq0 - 4 * h : -(1 << 30);  // keep q offsets >= rel
+        const int lim = qvalid - 32 * g - 4 * h;                            // keep q offsets < lim
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-          dv[dt] = mfma32(tr.read(Gs, 32 * w + 16 * j, dt), pb[j], dv[dt]);
-          dk[dt] = mfma32(tr.read(Qs, 32 * w + 16 * j, dt), db[j], dk[dt]);
+        for (int r = 0; r < 16; ++r) {
+          const int qoff = 8 * (r >> 2) + (r & 3);
+          s[r] = (qoff >= rel && qoff < lim) ? s[r] : -INFINITY;
         }
+      }
+      bf16x8 pb[2], db[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = exp2f_fast(s[r]);
+        dp[r] *= s[r];
+      }
+      pb[0] = pack8(s, 0);
+      pb[1] = pack8(s, 8);
+      db[0] = pack8(dp, 0);
+      db[1] = pack8(dp, 8);
+      bf16x8 tg[2], tq[2];
+      tg[0] = tr.read(Gs, 32 * g, 0);
+      tq[0] = tr.read(Qs, 32 * g, 0);
+#pragma unroll
+      for (int u = 0; u < 2 * NDT; ++u) {
+        const int j = u / NDT, dt = u % NDT, cur = u & 1;
+        if (u + 1 < 2 * NDT) {
+          const int j1 = (u + 1) / NDT, dt1 = (u + 1) % NDT;
+          tg[cur ^ 1] = tr.read(Gs, 32 * g + 16 * j1, dt1);
+          tq[cur ^ 1] = tr.read(Qs, 32 * g + 16 * j1, dt1);
+        }
+        dv[dt] = mfma32(tg[cur], pb[j], dv[dt]);
+        dk[dt] = mfma32(tq[cur], db[j], dk[dt]);
+      }
     }
     wait_vmem();
     __syncthreads();
   }
 
-  // Sum the four waves' partial dK^T / dV^T through LDS (all waves hold the same
-  // 32 kv columns); wave w then finishes d-tiles w, w + 4, ...
-  constexpr int NDT = D / 32;
-  float* red = reinterpret_cast<float*>(smem);  // [2][4 waves][NDT][16][64]
-  static_assert(2 * 4 * NDT * 16 * 64 * 4 <= 2 * STAGE * 2, "reduction fits the staging buffers");
+  // Sum the two q-group waves' partial dK^T (then dV^T) of each kv quarter
+  // through LDS; wave g of a quarter then owns d-tiles g, g + 2, ...  A whole
+  // tile (np == 1) is scaled and written as bf16; a piece of a split tile
+  // writes its fp32 sums to its slot ([dK | dV][kv row][d]) for
+  // attn_bwd_dkv_sum_kernel.
+  float* red = reinterpret_cast<float*>(smem);  // [2 g][4 kq][NDT][16][64]
+  const bool split = it.np > 1;
+  const bool slot_ok = split && it.slot0 >= 0 && (it.slot0 + it.np) * p.hkv <= kSplitSlots;
+  float* slot = p.dkv_part + (int64_t)((it.slot0 + it.piece) * p.hkv + hk) * (2 * BN * D);
+  const int64_t row = si.k_start + kvrow;
+  auto reduce = [&](const f32x16 (&acc)[NDT], int which) {
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      red[(((0 * 4 + w) * NDT + dt) * 16 + r) * 64 + lane] = dk[dt][r];
-      red[(((1 * 4 + w) * NDT + dt) * 16 + r) * 64 + lane] = dv[dt][r];
-    }
-  __syncthreads();
-  if (kvvalid) {
-    const int64_t row = si.k_start + kvrow;
-    for (int dt = w; dt < NDT; dt += 4) {
+      for (int r = 0; r < 16; ++r) red[(((g * 4 + kq) * NDT + dt) * 16 + r) * 64 + lane] = acc[dt][r];
+    __syncthreads();
+    for (int dt = g; dt < NDT; dt += 2) {
+      float sum[16];
 #pragma unroll
-      for (int which = 0; which < 2; ++which) {
-        float acc[16];
+      for (int r = 0; r < 16; ++r)
+        sum[r] = red[(((0 * 4 + kq) * NDT + dt) * 16 + r) * 64 + lane] +
+                 red[(((1 * 4 + kq) * NDT + dt) * 16 + r) * 64 + lane];
+      if (!split) {
+        if (kvvalid) {
+          bf16* dst = which == 0 ? p.dk + row * p.dk_tok + (int64_t)hk * p.dk_head
+                                 : p.dv + row * p.dv_tok + (int64_t)hk * p.dv_head;
+          const float sc = which == 0 ? p.scale : 1.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float a = 0.f;
+          for (int j = 0; j < 2; ++j) {
+            bf16x8 o;
 #pragma unroll
-          for (int ww = 0; ww < 4; ++ww) a += red[(((which * 4 + ww) * NDT + dt) * 16 + r) * 64 + lane];
-          acc[r] = a;
+            for (int q = 0; q < 8; ++q) o[q] = (bf16)(sum[8 * j + q] * sc);
+            st_bf16x8(dst + 32 * dt + 16 * j + 8 * h, o);
+          }
         }
-        const float sc = which == 0 ? p.scale : 1.f;
-        bf16* dst = which == 0 ? p.dk + row * p.dk_tok + (int64_t)hk * p.dk_head
-                               : p.dv + row * p.dv_tok + (int64_t)hk * p.dv_head;
+      } else if (slot_ok) {
+        float* dst = slot + ((int64_t)which * BN + 32 * kq + l32) * D + 32 * dt + 8 * h;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          bf16x8 o;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = (bf16)(acc[8 * j + i] * sc);
-          st_bf16x8(dst + 32 * dt + 16 * j + 8 * h, o);
+          *reinterpret_cast<f32x4*>(dst + 16 * j) = f32x4{sum[8 * j], sum[8 * j + 1], sum[8 * j + 2], sum[8 * j + 3]};
+          *reinterpret_cast<f32x4*>(dst + 16 * j + 4) =
+              f32x4{sum[8 * j + 4], sum[8 * j + 5], sum[8 * j + 6], sum[8 * j + 7]};
         }
       }
     }
+    __syncthreads();
+  };
+  reduce(dk, 0);
+  reduce(dv, 1);
+}
+
+// dK / dV of split tiles: the pieces' fp32 sums added in piece order (so the
+// result does not depend on which piece ran when), scaled and written as bf16.
+// One workgroup = one split tile and kv-head; thread x owns float4 column
+// x % (2 D / 4) of [dK | dV] and walks rows x / (2 D / 4), + 256 / (2 D / 4), ...
+template <int D>
+__global__ __launch_bounds__(256) void attn_bwd_dkv_sum_kernel(const AttnParams p) {
+  constexpr int BN = kBwdBN, C4 = D / 4, COLS = 2 * C4, RSTEP = 256 / COLS;
+  if ((int)blockIdx.x >= *p.nsplit) return;
+  const SplitTile st = p.splits[blockIdx.x];
+  const SeqInfo si = p.seq[st.b];
+  const int hk = blockIdx.y;
+  if ((st.slot0 + st.np) * p.hkv > kSplitSlots) return;
+  const int col = threadIdx.x % COLS, which = col / C4, c = col - which * C4;
+  const int k0 = st.t * BN;
+  const int rows = min(BN, si.k_len - k0);
+  const float* base = p.dkv_part + (int64_t)(st.slot0 * p.hkv + hk) * (2 * BN * D) + (int64_t)which * BN * D + 4 * c;
+  const int64_t pstride = (int64_t)p.hkv * (2 * BN * D);
+  const float sc = which == 0 ? p.scale : 1.f;
+  for (int r = threadIdx.x / COLS; r < rows; r += RSTEP) {
+    const float* src = base + (int64_t)r * D;
+    f32x4 acc = *reinterpret_cast<const f32x4*>(src);
+    for (int pc = 1; pc < st.np; ++pc) acc += *reinterpret_cast<const f32x4*>(src + pc * pstride);
+    const int64_t row = si.k_start + k0 + r;
+    bf16* dst = which == 0 ? p.dk + row * p.dk_tok + (int64_t)hk * p.dk_head + 4 * c
+                           : p.dv + row * p.dv_tok + (int64_t)hk * p.dv_head + 4 * c;
+    *reinterpret_cast<bf16x4*>(dst) = bf16x4{(bf16)(acc[0] * sc), (bf16)(acc[1] * sc), (bf16)(acc[2] * sc),
+                                             (bf16)(acc[3] * sc)};
   }
 }
 
@@ -243,10 +324,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnParams p) {
   tr.init(lane);
   const float c = p.scale_log2;
 
-  const int2 tl = p.qtiles[blockIdx.x];
+  // 1-D grid over (q tile, q-head), q-head fastest: the heads that share a
+  // kv-head read the same K / V blocks; each XCD gets runs of about 64
+  // entries (its resident workgroups), whole tiles at a time
+  const int e = xcd_order(blockIdx.x, gridDim.x, p.hq * max(1, 64 / p.hq));
+  const int ti = e / p.hq, hqi = e - ti * p.hq, hk = hqi / p.n_rep;
+  const int2 tl = p.qtiles[ti];
   if (tl.x < 0) return;
   const SeqInfo si = p.seq[tl.x];
-  const int hqi = blockIdx.y, hk = hqi / p.n_rep;
   const int q0 = tl.y * BM;
   const int off = si.k_len - si.q_len;
   int kv_end = si.k_len;
@@ -360,8 +445,10 @@ hipError_t launch_bwd_t(const AttnParams& p, int qcap, int kvcap, hipStream_t st
     if (blocks > 8192) blocks = 8192;
     hipLaunchKernelGGL((attn_bwd_preprocess_kernel<D>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
   }
-  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL>), dim3(kvcap, p.hkv), dim3(256), 0, stream, p);
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL>), dim3(qcap, p.hq), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)kvcap * p.hkv)), dim3(512), 0, stream,
+                     p);
+  hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D>), dim3(kMaxSplitTiles, p.hkv), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)qcap * p.hq)), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -50,10 +50,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   tr.init(lane);
   const float c = p.scale_log2;
 
-  const int2 tl = p.qtiles[blockIdx.x];
+  // 1-D grid over (q tile, q-head), q-head fastest: the heads that share a
+  // kv-head read the same K / V blocks; each XCD gets runs of about 64
+  // entries (its resident workgroups), whole tiles at a time
+  const int e = xcd_order(blockIdx.x, gridDim.x, p.hq * max(1, 64 / p.hq));
+  const int ti = e / p.hq, hqi = e - ti * p.hq, hk = hqi / p.n_rep;
+  const int2 tl = p.qtiles[ti];
   if (tl.x < 0) return;
   const SeqInfo si = p.seq[tl.x];
-  const int hqi = blockIdx.y, hk = hqi / p.n_rep;
   const int q0 = tl.y * BM;
   const int off = si.k_len - si.q_len;
   int kv_end = si.k_len;
@@ -194,7 +198,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
 
 template <int D, bool CAUSAL>
 hipError_t launch_fwd_t(const AttnParams& p, int qcap, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL>), dim3(qcap, p.hq), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)qcap * p.hq)), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -36,22 +36,32 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct AttnLayout {
-  size_t seq, qtiles, kvtiles, delta, total;
+  size_t seq, qtiles, kvitems, seqbuf, splits, nsplit, part, delta, lse2, total;
   int qcap, kvcap;
 };
 
-AttnLayout attn_layout(int batch, int64_t total_q, int64_t total_k, int hq, bool bwd) {
+AttnLayout attn_layout(int batch, int64_t total_q, int64_t total_k, int hq, int d, bool bwd) {
   AttnLayout L{};
   L.qcap = (int)siq::tile_cap(total_q, batch, siq::kFwdBM);
-  L.kvcap = bwd ? (int)siq::tile_cap(total_k, batch, siq::kBwdBN) : 0;
+  L.kvcap = bwd ? (int)siq::kv_item_cap(total_k, batch) : 0;
   size_t off = 0;
   L.seq = off;
   off += align256(sizeof(siq::SeqInfo) * (size_t)(batch > 0 ? batch : 1));
   L.qtiles = off;
   off += align256(sizeof(int2) * (size_t)L.qcap);
-  L.kvtiles = off;
-  off += align256(sizeof(int2) * (size_t)L.kvcap);
+  L.kvitems = off;
+  off += align256(sizeof(siq::KvItem) * (size_t)L.kvcap);
+  L.seqbuf = off;
+  if (bwd) off += align256(sizeof(int) * (1 + siq::kWorkBucketsMax) * (size_t)(batch > 0 ? batch : 1));
+  L.splits = off;
+  if (bwd) off += align256(sizeof(siq::SplitTile) * (size_t)siq::kMaxSplitTiles);
+  L.nsplit = off;
+  if (bwd) off += 256;
+  L.part = off;
+  if (bwd) off += align256(sizeof(float) * (size_t)siq::kSplitSlots * 2 * siq::kBwdBN * (size_t)d);
   L.delta = off;
+  if (bwd) off += align256(sizeof(float) * (size_t)hq * (size_t)total_q);
+  L.lse2 = off;
   if (bwd) off += align256(sizeof(float) * (size_t)hq * (size_t)total_q);
   L.total = off;
   return L;
@@ -94,16 +104,14 @@ const char* siq_last_error(void) { return g_last_error.c_str(); }
 
 size_t siq_attn_fwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d) {
   (void)hkv;
-  (void)d;
-  if (batch < 0 || total_q < 0 || total_k < 0 || hq <= 0) return 0;
-  return attn_layout(batch, total_q, total_k, hq, false).total;
+  if (batch < 0 || total_q < 0 || total_k < 0 || hq <= 0 || d <= 0) return 0;
+  return attn_layout(batch, total_q, total_k, hq, d, false).total;
 }
 
 size_t siq_attn_bwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d) {
   (void)hkv;
-  (void)d;
-  if (batch < 0 || total_q < 0 || total_k < 0 || hq <= 0) return 0;
-  return attn_layout(batch, total_q, total_k, hq, true).total;
+  if (batch < 0 || total_q < 0 || total_k < 0 || hq <= 0 || d <= 0) return 0;
+  return attn_layout(batch, total_q, total_k, hq, d, true).total;
 }
 
 int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, float* lse, const int32_t* cu_q,
@@ -120,7 +128,7 @@ int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, fl
   if (nq && (lse == nullptr || (reinterpret_cast<uintptr_t>(lse) & 3u)))
     return fail(SIQ_ERR_ALIGNMENT, "lse must be a non-NULL 4-byte aligned fp32 pointer");
   if (batch == 0 || total_q == 0) return ok();
-  const AttnLayout L = attn_layout(batch, total_q, total_k, hq, false);
+  const AttnLayout L = attn_layout(batch, total_q, total_k, hq, d, false);
   if (ws == nullptr || ws_bytes < L.total || !aligned16(ws))
     return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", L.total, ws_bytes);
 
@@ -151,9 +159,10 @@ int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, fl
   p.scale = scale;
   p.scale_log2 = scale * siq::kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0,
+  hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0, hq / hkv, hkv,
                                       reinterpret_cast<siq::SeqInfo*>(base + L.seq),
-                                      reinterpret_cast<int2*>(base + L.qtiles), L.qcap, nullptr, 0, s);
+                                      reinterpret_cast<int2*>(base + L.qtiles), L.qcap, nullptr, 0, nullptr,
+                                      nullptr, nullptr, s);
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
   e = siq::launch_attn_fwd(p, d, causal != 0, L.qcap, s);
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "attention forward launch failed: %s", hipGetErrorString(e));
@@ -177,7 +186,7 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
   if (nq && (lse == nullptr || (reinterpret_cast<uintptr_t>(lse) & 3u)))
     return fail(SIQ_ERR_ALIGNMENT, "lse must be a non-NULL 4-byte aligned fp32 pointer");
   if (batch == 0 || (total_q == 0 && total_k == 0)) return ok();
-  const AttnLayout L = attn_layout(batch, total_q, total_k, hq, true);
+  const AttnLayout L = attn_layout(batch, total_q, total_k, hq, d, true);
   if (ws == nullptr || ws_bytes < L.total || !aligned16(ws))
     return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", L.total, ws_bytes);
 
@@ -193,9 +202,13 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
   p.dk = static_cast<siq::bf16*>(dk);
   p.dv = static_cast<siq::bf16*>(dv);
   p.delta = reinterpret_cast<float*>(base + L.delta);
+  p.lse2 = reinterpret_cast<float*>(base + L.lse2);
   p.seq = reinterpret_cast<const siq::SeqInfo*>(base + L.seq);
   p.qtiles = reinterpret_cast<const int2*>(base + L.qtiles);
-  p.kvtiles = reinterpret_cast<const int2*>(base + L.kvtiles);
+  p.kvitems = reinterpret_cast<const siq::KvItem*>(base + L.kvitems);
+  p.dkv_part = reinterpret_cast<float*>(base + L.part);
+  p.splits = reinterpret_cast<const siq::SplitTile*>(base + L.splits);
+  p.nsplit = reinterpret_cast<const int*>(base + L.nsplit);
   p.batch = batch;
   p.hq = hq;
   p.hkv = hkv;
@@ -222,10 +235,13 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
   p.scale = scale;
   p.scale_log2 = scale * siq::kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0,
+  hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0, hq / hkv, hkv,
                                       reinterpret_cast<siq::SeqInfo*>(base + L.seq),
                                       reinterpret_cast<int2*>(base + L.qtiles), L.qcap,
-                                      reinterpret_cast<int2*>(base + L.kvtiles), L.kvcap, s);
+                                      reinterpret_cast<siq::KvItem*>(base + L.kvitems), L.kvcap,
+                                      reinterpret_cast<int*>(base + L.seqbuf),
+                                      reinterpret_cast<siq::SplitTile*>(base + L.splits),
+                                      reinterpret_cast<int*>(base + L.nsplit), s);
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
   e = siq::launch_attn_bwd(p, d, causal != 0, L.qcap, L.kvcap, s);
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "attention backward launch failed: %s", hipGetErrorString(e));

@@ -1,15 +1,22 @@
-// Device-side tile scheduler for varlen attention.
+// Device-side work scheduler for varlen attention.
 //
 // Packing puts sequences of very different lengths in one batch (a 16k-token
 // sequence next to 81-token image blocks).  Launching one workgroup per
 // (sequence, tile) in cu_seqlens order would leave the heaviest causal tiles
 // for last.  This kernel reads cu_seqlens on the device (no host sync), clamps
 // every extent to [0, total) so a malformed cu_seqlens can never drive a kernel
-// out of bounds, and writes the tile list ordered by decreasing work with a
-// counting sort.  The attention kernels then map blockIdx.x -> tile.
+// out of bounds, and writes the work lists ordered by decreasing work with a
+// counting sort.  The attention kernels then map blockIdx.x -> work.
 //
-// Block 0 builds the q-tile list (forward and dQ kernels), block 1 the kv-tile
-// list (dK/dV kernel).  Work keys are in units of 64 rows of the other side.
+// Block 0 builds the q-tile list of the forward and dQ kernels, heaviest
+// first (work key: kv rows seen, in units of 64).  Block 1 builds the dK/dV
+// work items: a kv tile has n_rep x (q blocks that can see it) steps; tiles
+// with more than S = max(kMinSplitSteps, hkv total / kSplitTarget) steps are
+// cut into pieces of at most S steps, so that the longest item stays near the
+// average load of a CU.  Items are ordered by sequence (longest first) and,
+// within a sequence, piece-major, so that the items that run side by side on
+// an XCD read the same Q / dO blocks at the same time; split tiles are listed
+// for the kernel that adds their partial sums.
 #include "attn.h"
 
 namespace siq {
@@ -31,20 +38,33 @@ __device__ __forceinline__ SeqInfo seq_extent(const int* cu_q, const int* cu_k, 
   return s;
 }
 
-// Rows of the other side that tile t touches (causal alignment is bottom-right:
-// q row i sees k rows <= i + (Lk - Lq)).
-__device__ __forceinline__ int tile_key(const SeqInfo& s, int t, int mode, int causal) {
+// kv rows that q tile t sees (causal alignment is bottom-right: q row i sees
+// k rows <= i + (Lk - Lq)), in units of 64.
+__device__ __forceinline__ int q_tile_key(const SeqInfo& s, int t, int causal) {
   const int off = s.k_len - s.q_len;
-  int n;
-  if (mode == 0) {
-    n = s.k_len;
-    if (causal) n = max(0, min(s.k_len, (t + 1) * kFwdBM + off));
-  } else {
-    n = s.q_len;
-    if (causal) n = max(0, s.q_len - max(0, t * kBwdBN - off));
-  }
+  int n = s.k_len;
+  if (causal) n = max(0, min(s.k_len, (t + 1) * kFwdBM + off));
   const int key = (n + 63) >> 6;
   return key < kSchedKeys - 1 ? key : kSchedKeys - 1;
+}
+
+// dK/dV steps of kv tile t: n_rep x the q blocks of kBwdBM rows that can see
+// any of its rows (the dK/dV kernel walks exactly these, in this order).
+__device__ __forceinline__ int kv_tile_steps(const SeqInfo& s, int t, int causal, int n_rep) {
+  const int off = s.k_len - s.q_len;
+  const int qb0 = causal ? max(0, t * kBwdBN - off) / kBwdBM : 0;
+  const int nqb = s.q_len > qb0 * kBwdBM ? (s.q_len - qb0 * kBwdBM + kBwdBM - 1) / kBwdBM : 0;
+  return nqb * n_rep;
+}
+
+__device__ __forceinline__ int clamp_key(int w) { return w < kSchedKeys - 1 ? w : kSchedKeys - 1; }
+
+// dK/dV items are sorted into kWorkBuckets classes of step count, heaviest
+// class first (class 0 holds the full pieces of S steps).
+constexpr int kWorkBuckets = kWorkBucketsMax;
+__device__ __forceinline__ int work_bucket(int w, int S) {
+  const int k = (int)(((long long)(S - w) * kWorkBuckets) / (S + 1));
+  return k < 0 ? 0 : (k > kWorkBuckets - 1 ? kWorkBuckets - 1 : k);
 }
 
 __device__ int block_exclusive_scan(int* buf, int n, int* wsum) {
@@ -79,52 +99,195 @@ __device__ int block_exclusive_scan(int* buf, int n, int* wsum) {
   return total;
 }
 
+// In-place exclusive scan of a global array of any length, 2 kSchedThreads
+// entries at a time through `buf` (LDS); returns the total.
+__device__ int scan_global(int* a, int n, int* buf, int* wsum) {
+  const int tid = threadIdx.x;
+  int carry = 0;
+  for (int c0 = 0; c0 < n; c0 += 2 * kSchedThreads) {
+    const int m = min(2 * kSchedThreads, n - c0);
+    for (int i = tid; i < m; i += kSchedThreads) buf[i] = a[c0 + i];
+    __syncthreads();
+    const int tot = block_exclusive_scan(buf, m, wsum);
+    for (int i = tid; i < m; i += kSchedThreads) a[c0 + i] = buf[i] + carry;
+    carry += tot;
+    __threadfence_block();
+    __syncthreads();
+  }
+  return carry;
+}
+
 __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __restrict__ cu_q,
                                                                  const int* __restrict__ cu_k, int batch,
                                                                  int64_t total_q, int64_t total_k, int causal,
-                                                                 SeqInfo* __restrict__ seq,
+                                                                 int n_rep, int hkv, SeqInfo* __restrict__ seq,
                                                                  int2* __restrict__ qtiles, int qcap,
-                                                                 int2* __restrict__ kvtiles, int kvcap) {
+                                                                 KvItem* __restrict__ kvitems, int kvcap,
+                                                                 int* __restrict__ seqbuf,
+                                                                 SplitTile* __restrict__ splits,
+                                                                 int* __restrict__ nsplit) {
   __shared__ int hist[kSchedKeys];
   __shared__ int wsum[kSchedThreads / 64 + 1];
-  const int mode = blockIdx.x;
-  int2* tiles = mode == 0 ? qtiles : kvtiles;
-  const int cap = mode == 0 ? qcap : kvcap;
-  const int rows = mode == 0 ? kFwdBM : kBwdBN;
-  if (tiles == nullptr) return;
+  __shared__ long long wsteps[kSchedThreads / 64];
+  __shared__ int nslot, nsplit_sh;
   const int tid = threadIdx.x;
 
   for (int i = tid; i < kSchedKeys; i += kSchedThreads) hist[i] = 0;
-  __syncthreads();
-  for (int b = tid; b < batch; b += kSchedThreads) {
-    const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
-    if (mode == 0) seq[b] = s;
-    const int len = mode == 0 ? s.q_len : s.k_len;
-    const int nt = (len + rows - 1) / rows;
-    for (int t = 0; t < nt; ++t) atomicAdd(&hist[kSchedKeys - 1 - tile_key(s, t, mode, causal)], 1);
+  if (tid == 0) {
+    nslot = 0;
+    nsplit_sh = 0;
   }
   __syncthreads();
-  const int total = block_exclusive_scan(hist, kSchedKeys, wsum);
+
+  if (blockIdx.x == 0) {
+    // q tiles of the forward / dQ kernels, heaviest first
+    for (int b = tid; b < batch; b += kSchedThreads) {
+      const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
+      seq[b] = s;
+      const int nt = (s.q_len + kFwdBM - 1) / kFwdBM;
+      for (int t = 0; t < nt; ++t) atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(s, t, causal)], 1);
+    }
+    __syncthreads();
+    const int total = block_exclusive_scan(hist, kSchedKeys, wsum);
+    for (int b = tid; b < batch; b += kSchedThreads) {
+      const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
+      const int nt = (s.q_len + kFwdBM - 1) / kFwdBM;
+      for (int t = 0; t < nt; ++t) {
+        const int pos = atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(s, t, causal)], 1);
+        if (pos < qcap) qtiles[pos] = make_int2(b, t);
+      }
+    }
+    for (int i = total + tid; i < qcap; i += kSchedThreads) qtiles[i] = make_int2(-1, -1);
+    return;
+  }
+
+  // dK/dV work items.  1: total steps over all kv tiles (per kv-head).
+  long long mine = 0;
   for (int b = tid; b < batch; b += kSchedThreads) {
     const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
-    const int len = mode == 0 ? s.q_len : s.k_len;
-    const int nt = (len + rows - 1) / rows;
+    const int nt = (s.k_len + kBwdBN - 1) / kBwdBN;
+    for (int t = 0; t < nt; ++t) mine += kv_tile_steps(s, t, causal, n_rep);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mine += __shfl_xor(mine, o);
+  if ((tid & 63) == 0) wsteps[tid >> 6] = mine;
+  __syncthreads();
+  long long steps = 0;
+  for (int i = 0; i < kSchedThreads / 64; ++i) steps += wsteps[i];
+  // 2: piece length S >= hkv * steps / kSplitTarget, so that the split pieces
+  // (each kv-head counted) number at most 2 kSplitTarget and the items at most
+  // kSplitTarget more than the tiles.
+  long long sl = (steps * hkv + kSplitTarget - 1) / kSplitTarget;
+  if (sl < kMinSplitSteps) sl = kMinSplitSteps;
+  if (sl > (1 << 30)) sl = 1 << 30;
+  const int S = (int)sl;
+
+  // 3: sequences by decreasing kv length (counting sort on 64-row units)
+  int* order = seqbuf;         // [batch] rank -> sequence
+  int* start = seqbuf + batch;  // [kWorkBuckets][batch] first position of (bucket, rank)
+  for (int b = tid; b < batch; b += kSchedThreads) {
+    const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
+    atomicAdd(&hist[kSchedKeys - 1 - clamp_key((s.k_len + 63) >> 6)], 1);
+  }
+  __syncthreads();
+  block_exclusive_scan(hist, kSchedKeys, wsum);
+  for (int b = tid; b < batch; b += kSchedThreads) {
+    const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
+    order[atomicAdd(&hist[kSchedKeys - 1 - clamp_key((s.k_len + 63) >> 6)], 1)] = b;
+  }
+  __threadfence_block();
+  __syncthreads();
+
+  // 4: item positions, a stable sort by (work bucket, heaviest first; sequence
+  // rank; piece; tile): the list stays close to longest-first, and the items of
+  // one bucket that sit side by side (one XCD's run) share a sequence and a
+  // piece index, i.e. they walk the same q blocks at the same time
+  for (int r = tid; r < batch; r += kSchedThreads) {
+    const SeqInfo s = seq_extent(cu_q, cu_k, order[r], total_q, total_k);
+    const int nt = (s.k_len + kBwdBN - 1) / kBwdBN;
+    int cnt[kWorkBuckets];
+#pragma unroll
+    for (int k = 0; k < kWorkBuckets; ++k) cnt[k] = 0;
     for (int t = 0; t < nt; ++t) {
-      const int pos = atomicAdd(&hist[kSchedKeys - 1 - tile_key(s, t, mode, causal)], 1);
-      if (pos < cap) tiles[pos] = make_int2(b, t);
+      const int w = kv_tile_steps(s, t, causal, n_rep);
+      const int np = w > S ? (w + S - 1) / S : 1;
+      for (int pc = 0; pc < np; ++pc) {
+        const int bk = work_bucket(min(S, w - pc * S), S);
+#pragma unroll
+        for (int k = 0; k < kWorkBuckets; ++k) cnt[k] += k == bk;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kWorkBuckets; ++k) start[k * batch + r] = cnt[k];
+  }
+  __threadfence_block();
+  __syncthreads();
+  const int total = scan_global(start, kWorkBuckets * batch, hist, wsum);
+
+  // 5: write the items; split tiles get consecutive partial slots and a
+  // SplitTile entry
+  for (int r = tid; r < batch; r += kSchedThreads) {
+    const int b = order[r];
+    const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
+    const int nt = (s.k_len + kBwdBN - 1) / kBwdBN;
+    int nsl = 0, maxnp = 1;
+    for (int t = 0; t < nt; ++t) {
+      const int w = kv_tile_steps(s, t, causal, n_rep);
+      const int np = w > S ? (w + S - 1) / S : 1;
+      if (np > 1) nsl += np;
+      maxnp = max(maxnp, np);
+    }
+    const int slot_base = nsl > 0 ? atomicAdd(&nslot, nsl) : 0;
+    int pos[kWorkBuckets];
+#pragma unroll
+    for (int k = 0; k < kWorkBuckets; ++k) pos[k] = start[k * batch + r];
+    for (int pc = 0; pc < maxnp; ++pc) {
+      int slot = slot_base;
+      for (int t = 0; t < nt; ++t) {
+        const int w = kv_tile_steps(s, t, causal, n_rep);
+        const int np = w > S ? (w + S - 1) / S : 1;
+        const int slot0 = np > 1 ? slot : -1;
+        if (np > 1) slot += np;
+        if (pc >= np) continue;
+        if (pc == 0 && np > 1) {
+          const int k = atomicAdd(&nsplit_sh, 1);
+          if (k < kMaxSplitTiles) splits[k] = SplitTile{b, t, np, slot0};
+        }
+        KvItem it;
+        it.b = b;
+        it.t = t;
+        it.s0 = pc * S;
+        it.s1 = min(w, (pc + 1) * S);
+        it.piece = pc;
+        it.np = np;
+        it.slot0 = slot0;
+        it.pad = 0;
+        const int bk = work_bucket(it.s1 - it.s0, S);
+        int at = 0;
+#pragma unroll
+        for (int k = 0; k < kWorkBuckets; ++k)
+          if (k == bk) at = pos[k]++;
+        if (at < kvcap) kvitems[at] = it;
+      }
     }
   }
-  for (int i = total + tid; i < cap; i += kSchedThreads) tiles[i] = make_int2(-1, -1);
+  for (int i = total + tid; i < kvcap; i += kSchedThreads) {
+    KvItem it{};
+    it.b = -1;
+    kvitems[i] = it;
+  }
+  __syncthreads();
+  if (tid == 0) *nsplit = min(nsplit_sh, kMaxSplitTiles);
 }
 
 }  // namespace
 
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,
-                           int causal, SeqInfo* seq, int2* qtiles, int qcap, int2* kvtiles, int kvcap,
-                           hipStream_t stream) {
-  const int blocks = kvtiles != nullptr ? 2 : 1;
+                           int causal, int n_rep, int hkv, SeqInfo* seq, int2* qtiles, int qcap, KvItem* kvitems,
+                           int kvcap, int* seqbuf, SplitTile* splits, int* nsplit, hipStream_t stream) {
+  const int blocks = kvitems != nullptr ? 2 : 1;
   hipLaunchKernelGGL(schedule_kernel, dim3(blocks), dim3(kSchedThreads), 0, stream, cu_q, cu_k, batch, total_q,
-                     total_k, causal, seq, qtiles, qcap, kvtiles, kvcap);
+                     total_k, causal, n_rep, hkv, seq, qtiles, qcap, kvitems, kvcap, seqbuf, splits, nsplit);
   return hipGetLastError();
 }
 

@@ -77,24 +77,29 @@ struct LdsTile {
         const int r = i * RPI + lrow;
         o = r < nrows ? o : o - (uint32_t)((r - nrows + 1) * stride);
       }
-      __builtin_amdgcn_global_load_lds(gbase + o, (lds_void*)(lds + i * 512), 16, 0, 0);
+      // uniform base + 32-bit byte offset: the saddr + voffset form
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(gbase) + (o << 1), (lds_void*)(lds + i * 512),
+                                       16, 0, 0);
     }
   }
 };
 
 // Row operand reads: lane l reads row (rbase + l % 32), logical chunk
-// 2 ks + h (d = 16 ks + 8 h .. +7), for ks = 0 .. D/16 - 1.  The swizzled chunk
-// offsets depend only on (l % 32) because row bases are multiples of 32.
+// 2 ks + h (d = 16 ks + 8 h .. +7), for ks = 0 .. D/16 - 1.  The swizzle XORs
+// bits below the row offset, so the element offset of chunk 2 ks + h is
+// base ^ 16 ks with base = (l % 32) D + 8 (swz(l % 32) ^ h): one register per
+// lane (row bases are multiples of 32 rows).
 template <int D>
 struct RowRead {
-  uint32_t off[D / 16];  // element offsets within a 32-row block
+  uint32_t base;
   __device__ __forceinline__ void init(int lane) {
-    const int l32 = lane & 31, h = lane >> 5, f = swz<D>(l32);
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) off[ks] = (uint32_t)(l32 * D + (((2 * ks + h) ^ f) << 3));
+    const int l32 = lane & 31, h = lane >> 5;
+    base = (uint32_t)(l32 * D + 8 * (swz<D>(l32) ^ h));
   }
   // T: tile base, rb: first row of the 32-row block (multiple of 32)
-  __device__ __forceinline__ bf16x8 read(const bf16* T, int rb, int ks) const { return ld_bf16x8(T + rb * D + off[ks]); }
+  __device__ __forceinline__ bf16x8 read(const bf16* T, int rb, int ks) const {
+    return ld_bf16x8(T + rb * D + (base ^ (uint32_t)(16 * ks)));
+  }
 };
 
 // Transposed operand reads with ds_read_b64_tr_b16.  Within each 16-lane
@@ -111,7 +116,10 @@ struct RowRead {
 // multiple of 16.
 template <int D>
 struct TrRead {
-  uint32_t off[2][D / 32];
+  // element offset of (row r_e, 32-column block 0) for the lane's two 4-row
+  // groups e; the block dt is reached by XOR with 32 dt (the swizzle only
+  // touches chunk bits below the row offset)
+  uint32_t base[2];
   __device__ __forceinline__ void init(int lane) {
     const int G = lane >> 4, p = lane & 15, j = p >> 2, q = p & 3;
     const int cl = 2 * (G & 1) + (q & 1);  // logical chunk within a 32-column block
@@ -119,21 +127,27 @@ struct TrRead {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int r = 4 * (G >> 1) + j + 8 * e;
-      const int f = swz<D>(r);
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) off[e][dt] = (uint32_t)(r * D + (((4 * dt + cl) ^ f) << 3) + wo);
+      base[e] = (uint32_t)(r * D + 8 * (cl ^ swz<D>(r)) + wo);
     }
   }
   __device__ __forceinline__ bf16x8 read(const bf16* T, int k0, int dt) const {
-    const bf16* base = T + k0 * D;
-    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + off[0][dt]));
-    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + off[1][dt]));
+    const bf16* t = T + k0 * D;
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(t + (base[0] ^ (uint32_t)(32 * dt))));
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(t + (base[1] ^ (uint32_t)(32 * dt))));
     return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
 };
 
 // Wait for this wave's outstanding global (and direct-to-LDS) loads.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Wait until at most N of this wave's global loads are outstanding (loads
+// complete in issue order, so everything but the newest N has landed).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
 
 // Per-sequence extents, clamped on the device to [0, total).
 struct SeqInfo {
