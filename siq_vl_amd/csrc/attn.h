@@ -17,17 +17,15 @@ constexpr int kSchedKeys = 2048;
 // in one workgroup unless the tile is heavier than total / kSplitTarget steps;
 // heavier tiles are cut into pieces whose fp32 partial sums are added, in
 // piece order, by a small kernel after the dK/dV kernel.
-constexpr int kSplitTarget = 384;
+constexpr int kSplitTarget = 256;
 constexpr int kMinSplitSteps = 4;
 constexpr int kSplitSlots = 2 * kSplitTarget + 2;  // bound on sum(pieces x hkv) over split tiles
 constexpr int kMaxSplitTiles = kSplitSlots / 2;    // a split tile has >= 2 pieces
 constexpr int kXcds = 8;                           // MI355X: workgroup b runs on XCD b % 8
-constexpr int kWorkBucketsMax = 16;                // scheduler scratch: work classes x batch ints
 
 // One dK/dV work item: steps [s0, s1) of kv tile t of sequence b; piece `piece`
 // of np (np == 1: the whole tile, written directly as bf16).  Steps walk the
-// q blocks downwards from the last one, each over the n_rep q-heads, so the
-// tiles of one sequence read the same Q / dO block at the same step.  A piece
+// q blocks downwards from the last one, each over the n_rep q-heads.  A piece
 // of a split tile writes fp32 sums to slot (slot0 + piece) * hkv + hk.
 struct KvItem {
   int b, t, s0, s1, piece, np, slot0, pad;

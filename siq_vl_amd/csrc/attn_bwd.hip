@@ -21,10 +21,12 @@
 //    quarter are summed through LDS.  Tiles heavier than the scheduler's
 //    piece length run as several work items writing fp32 sums to workspace
 //    slots, which a small kernel adds in piece order afterwards.
-//  * dQ: one workgroup = 128 q rows of one q-head (same schedule as the
-//    forward); Q and dO in registers as B operands of S^T = K Q^T and
-//    dP^T = V dO^T, K and V tiles row-major in LDS, dQ^T += K^T dS^T with K^T
-//    read by ds_read_b64_tr_b16.
+//  * dQ: one workgroup = 4 waves = 128 q rows of one q-head (same schedule as
+//    the forward); wave g owns q rows 32 g .. 32 g + 31 with Q and dO in
+//    registers as B operands of S^T = K Q^T and dP^T = V dO^T.  K and V tiles
+//    of 64 rows are double-buffered row-major in LDS and taken 32 rows at a
+//    time (operand reads one k-step ahead of the MFMAs); dQ^T += K^T dS^T reads
+//    K^T with ds_read_b64_tr_b16.
 #include "attn.h"
 
 namespace siq {
@@ -279,10 +281,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
 // dK / dV of split tiles: the pieces' fp32 sums added in piece order (so the
 // result does not depend on which piece ran when), scaled and written as bf16.
 // One workgroup = one split tile and kv-head; thread x owns float4 column
-// x % (2 D / 4) of [dK | dV] and walks rows x / (2 D / 4), + 256 / (2 D / 4), ...
+// x % (2 D / 4) of [dK | dV] and rows x / (2 D / 4) + RSTEP i, 8 rows at a
+// time so that their loads are in flight together.
 template <int D>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_sum_kernel(const AttnParams p) {
-  constexpr int BN = kBwdBN, C4 = D / 4, COLS = 2 * C4, RSTEP = 256 / COLS;
+  constexpr int BN = kBwdBN, C4 = D / 4, COLS = 2 * C4, RSTEP = 256 / COLS, U = 8;
+  static_assert(BN % (RSTEP * U) == 0, "rows split evenly");
   if ((int)blockIdx.x >= *p.nsplit) return;
   const SplitTile st = p.splits[blockIdx.x];
   const SeqInfo si = p.seq[st.b];
@@ -294,27 +298,38 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_sum_kernel(const AttnParams 
   const float* base = p.dkv_part + (int64_t)(st.slot0 * p.hkv + hk) * (2 * BN * D) + (int64_t)which * BN * D + 4 * c;
   const int64_t pstride = (int64_t)p.hkv * (2 * BN * D);
   const float sc = which == 0 ? p.scale : 1.f;
-  for (int r = threadIdx.x / COLS; r < rows; r += RSTEP) {
-    const float* src = base + (int64_t)r * D;
-    f32x4 acc = *reinterpret_cast<const f32x4*>(src);
-    for (int pc = 1; pc < st.np; ++pc) acc += *reinterpret_cast<const f32x4*>(src + pc * pstride);
-    const int64_t row = si.k_start + k0 + r;
-    bf16* dst = which == 0 ? p.dk + row * p.dk_tok + (int64_t)hk * p.dk_head + 4 * c
-                           : p.dv + row * p.dv_tok + (int64_t)hk * p.dv_head + 4 * c;
-    *reinterpret_cast<bf16x4*>(dst) = bf16x4{(bf16)(acc[0] * sc), (bf16)(acc[1] * sc), (bf16)(acc[2] * sc),
-                                             (bf16)(acc[3] * sc)};
+  for (int r0 = threadIdx.x / COLS; r0 < BN; r0 += RSTEP * U) {
+    f32x4 acc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] = *reinterpret_cast<const f32x4*>(base + (int64_t)(r0 + RSTEP * u) * D);
+    for (int pc = 1; pc < st.np; ++pc)
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        acc[u] += *reinterpret_cast<const f32x4*>(base + pc * pstride + (int64_t)(r0 + RSTEP * u) * D);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int r = r0 + RSTEP * u;
+      if (r >= rows) continue;
+      const int64_t row = si.k_start + k0 + r;
+      bf16* dst = which == 0 ? p.dk + row * p.dk_tok + (int64_t)hk * p.dk_head + 4 * c
+                             : p.dv + row * p.dv_tok + (int64_t)hk * p.dv_head + 4 * c;
+      *reinterpret_cast<bf16x4*>(dst) = bf16x4{(bf16)(acc[u][0] * sc), (bf16)(acc[u][1] * sc), (bf16)(acc[u][2] * sc),
+                                               (bf16)(acc[u][3] * sc)};
+    }
   }
 }
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnParams p) {
-  constexpr int BM = kFwdBM, BN = kFwdBN, NT = 256;
-  using Tile = LdsTile<BN, D, NT / 64>;
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p) {
+  constexpr int BM = kFwdBM, BN = kFwdBN, NT = 256, NW = NT / 64;
+  static_assert(BM == 128 && BN == 64, "128 q rows (4 x 32) by 64 kv rows (2 x 32) per step");
+  using Tile = LdsTile<BN, D, NW>;
   constexpr int TE = Tile::ELEMS, STAGE = 2 * TE;  // K, V
+  constexpr int NDT = D / 32;
   __shared__ __align__(16) bf16 smem[2 * STAGE];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
-  const int wu = wave_uniform(w);
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int g = wave_uniform(tid >> 6);  // q group: rows 32 g .. 32 g + 31 of the tile
   Tile kt, vt;
   kt.init(p.k_tok, lane);
   vt.init(p.v_tok, lane);
@@ -338,9 +353,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnParams p) {
   if (CAUSAL) kv_end = min(kv_end, q0 + BM + off);
   const int nblk = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
 
-  const int qrow = q0 + 32 * w + l32;
+  const int qrow = q0 + 32 * g + l32;
   const bool qvalid = qrow < si.q_len;
-  const int lim = CAUSAL ? min(si.k_len - 1, qrow + off) : si.k_len - 1;
+  const int lim = CAUSAL ? min(si.k_len - 1, qrow + off) : si.k_len - 1;  // last kv row qrow sees
   bf16x8 qf[D / 16], gf[D / 16];
   float lse2, dlt;
   {
@@ -354,68 +369,75 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnParams p) {
       gf[ks] = qvalid ? b : zero_bf16x8();
     }
     const int64_t idx = (int64_t)hqi * p.lse_head + r;
-    const float l = p.lse[idx], dl = p.delta[idx];
-    lse2 = qvalid ? l * kLog2e : INFINITY;
+    const float l2 = p.lse2[idx], dl = p.delta[idx];
+    lse2 = qvalid ? l2 : INFINITY;
     dlt = qvalid ? dl : 0.f;
   }
-  f32x16 dq[D / 32];
+  f32x16 dq[NDT];
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) dq[i] = zero16();
+  for (int i = 0; i < NDT; ++i) dq[i] = zero16();
 
   const bf16* kbase = p.k + (int64_t)si.k_start * p.k_tok + (int64_t)hk * p.k_head;
   const bf16* vbase = p.v + (int64_t)si.k_start * p.v_tok + (int64_t)hk * p.v_head;
-  if (nblk > 0) {
-    kt.issue(kbase, p.k_tok, si.k_len, smem, wu);
-    vt.issue(vbase, p.v_tok, si.k_len, smem + TE, wu);
-  }
+  auto issue = [&](int kb, int buf) {
+    kt.issue(kbase + (int64_t)(kb * BN) * p.k_tok, p.k_tok, si.k_len - kb * BN, smem + buf * STAGE, g);
+    vt.issue(vbase + (int64_t)(kb * BN) * p.v_tok, p.v_tok, si.k_len - kb * BN, smem + buf * STAGE + TE, g);
+  };
+  if (nblk > 0) issue(0, 0);
   wait_vmem();
   __syncthreads();
 
-  const int wq_last = q0 + 32 * w + 31;
+  const int wq0 = q0 + 32 * g;
   for (int kb = 0; kb < nblk; ++kb) {
     const bf16* Ks = smem + (kb & 1) * STAGE;
     const bf16* Vs = Ks + TE;
-    const int k0 = kb * BN;
-    const bool more = kb + 1 < nblk;
-    if (more) {
-      bf16* nx = smem + ((kb + 1) & 1) * STAGE;
-      kt.issue(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN, nx, wu);
-      vt.issue(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN, nx + TE, wu);
-    }
-    const bool active = !CAUSAL || (k0 <= wq_last + off);
+    if (kb + 1 < nblk) issue(kb + 1, (kb + 1) & 1);
+    // the step's two 32-row kv halves in turn
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+    const int kw = kb * BN + 32 * kh;  // first kv row of this half
+    const bool active = kw < si.k_len && (!CAUSAL || kw <= wq0 + 31 + off);
     if (active) {
-      const bool need_mask = (k0 + BN > si.k_len) || (CAUSAL && k0 + BN - 1 > q0 + 32 * w + off);
-      // accumulator (t, r) holds kv = k0 + 32t + nrow(r, h) for q = qrow
-      f32x16 s[BN / 32], dp[BN / 32];
+      // accumulator r holds kv = kw + nrow(r, h) for q = qrow (operands one k-step ahead)
+      f32x16 s = zero16(), dp = zero16();
+      bf16x8 fk[2], fv[2];
+      fk[0] = rr.read(Ks, 32 * kh, 0);
+      fv[0] = rr.read(Vs, 32 * kh, 0);
 #pragma unroll
-      for (int t = 0; t < BN / 32; ++t) {
-        s[t] = zero16();
-        dp[t] = zero16();
+      for (int ks = 0; ks < D / 16; ++ks) {
+        const int cur = ks & 1;
+        if (ks + 1 < D / 16) {
+          fk[cur ^ 1] = rr.read(Ks, 32 * kh, ks + 1);
+          fv[cur ^ 1] = rr.read(Vs, 32 * kh, ks + 1);
+        }
+        s = mfma32(fk[cur], qf[ks], s);
+        dp = mfma32(fv[cur], gf[ks], dp);
       }
 #pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks)
+      for (int r = 0; r < 16; ++r) {
+        s[r] = __builtin_fmaf(s[r], c, -lse2);
+        dp[r] -= dlt;
+      }
+      if (kw + 31 > si.k_len - 1 || (CAUSAL && kw + 31 > wq0 + off)) {
+        // kv rows past the end of the sequence or after the causal limit of some row
+        const int rel = lim - kw - 4 * h;  // keep kv offsets <= rel
 #pragma unroll
-        for (int t = 0; t < BN / 32; ++t) {
-          s[t] = mfma32(rr.read(Ks, 32 * t, ks), qf[ks], s[t]);
-          dp[t] = mfma32(rr.read(Vs, 32 * t, ks), gf[ks], dp[t]);
-        }
-      const int rel = lim - k0 - 4 * h;
-      bf16x8 db[BN / 16];
-#pragma unroll
-      for (int t = 0; t < BN / 32; ++t) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float pv = exp2f_fast(__builtin_fmaf(s[t][r], c, -lse2));
-          if (need_mask) pv = (32 * t + 8 * (r >> 2) + (r & 3) > rel) ? 0.f : pv;
-          dp[t][r] = pv * (dp[t][r] - dlt);
-        }
-        db[2 * t] = pack8(dp[t], 0);
-        db[2 * t + 1] = pack8(dp[t], 8);
+        for (int r = 0; r < 16; ++r) s[r] = (8 * (r >> 2) + (r & 3) > rel) ? -INFINITY : s[r];
       }
 #pragma unroll
-      for (int st = 0; st < BN / 16; ++st)
+      for (int r = 0; r < 16; ++r) dp[r] *= exp2f_fast(s[r]);
+      bf16x8 db[2];
+      db[0] = pack8(dp, 0);
+      db[1] = pack8(dp, 8);
+      bf16x8 tk[2];
+      tk[0] = tr.read(Ks, 32 * kh, 0);
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) dq[dt] = mfma32(tr.read(Ks, 16 * st, dt), db[st], dq[dt]);
+      for (int u = 0; u < 2 * NDT; ++u) {
+        const int sub = u / NDT, dt = u % NDT, cur = u & 1;
+        if (u + 1 < 2 * NDT) tk[cur ^ 1] = tr.read(Ks, 32 * kh + 16 * ((u + 1) / NDT), (u + 1) % NDT);
+        dq[dt] = mfma32(tk[cur], db[sub], dq[dt]);
+      }
+    }
     }
     wait_vmem();
     __syncthreads();
@@ -424,7 +446,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnParams p) {
   if (qvalid) {
     bf16* dqp = p.dq + (int64_t)(si.q_start + qrow) * p.dq_tok + (int64_t)hqi * p.dq_head;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
+    for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         bf16x8 a;

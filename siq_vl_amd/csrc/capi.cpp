@@ -52,7 +52,7 @@ AttnLayout attn_layout(int batch, int64_t total_q, int64_t total_k, int hq, int 
   L.kvitems = off;
   off += align256(sizeof(siq::KvItem) * (size_t)L.kvcap);
   L.seqbuf = off;
-  if (bwd) off += align256(sizeof(int) * (1 + siq::kWorkBucketsMax) * (size_t)(batch > 0 ? batch : 1));
+  if (bwd) off += align256(sizeof(int) * ((size_t)(batch > 0 ? batch : 1) + 1));
   L.splits = off;
   if (bwd) off += align256(sizeof(siq::SplitTile) * (size_t)siq::kMaxSplitTiles);
   L.nsplit = off;

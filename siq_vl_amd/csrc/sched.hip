@@ -13,10 +13,8 @@
 // work items: a kv tile has n_rep x (q blocks that can see it) steps; tiles
 // with more than S = max(kMinSplitSteps, hkv total / kSplitTarget) steps are
 // cut into pieces of at most S steps, so that the longest item stays near the
-// average load of a CU.  Items are ordered by sequence (longest first) and,
-// within a sequence, piece-major, so that the items that run side by side on
-// an XCD read the same Q / dO blocks at the same time; split tiles are listed
-// for the kernel that adds their partial sums.
+// average load of a CU; the pieces are placed heaviest first, and split tiles
+// are listed for the kernel that adds their partial sums.
 #include "attn.h"
 
 namespace siq {
@@ -58,14 +56,6 @@ __device__ __forceinline__ int kv_tile_steps(const SeqInfo& s, int t, int causal
 }
 
 __device__ __forceinline__ int clamp_key(int w) { return w < kSchedKeys - 1 ? w : kSchedKeys - 1; }
-
-// dK/dV items are sorted into kWorkBuckets classes of step count, heaviest
-// class first (class 0 holds the full pieces of S steps).
-constexpr int kWorkBuckets = kWorkBucketsMax;
-__device__ __forceinline__ int work_bucket(int w, int S) {
-  const int k = (int)(((long long)(S - w) * kWorkBuckets) / (S + 1));
-  return k < 0 ? 0 : (k > kWorkBuckets - 1 ? kWorkBuckets - 1 : k);
-}
 
 __device__ int block_exclusive_scan(int* buf, int n, int* wsum) {
   // buf[0..n) -> exclusive prefix sums; returns the total.  n <= 2 * kSchedThreads.
@@ -161,19 +151,28 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
     return;
   }
 
-  // dK/dV work items.  1: total steps over all kv tiles (per kv-head).
+  // dK/dV work items.  1: kv tiles per sequence (prefix sums) and the total
+  // number of steps (per kv-head).
+  int* tfirst = seqbuf;  // [batch + 1] first flattened kv tile of each sequence
   long long mine = 0;
   for (int b = tid; b < batch; b += kSchedThreads) {
     const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
     const int nt = (s.k_len + kBwdBN - 1) / kBwdBN;
+    tfirst[b] = nt;
     for (int t = 0; t < nt; ++t) mine += kv_tile_steps(s, t, causal, n_rep);
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mine += __shfl_xor(mine, o);
   if ((tid & 63) == 0) wsteps[tid >> 6] = mine;
+  __threadfence_block();
   __syncthreads();
   long long steps = 0;
   for (int i = 0; i < kSchedThreads / 64; ++i) steps += wsteps[i];
+  const int ntiles = scan_global(tfirst, batch, hist, wsum);
+  if (tid == 0) tfirst[batch] = ntiles;
+  for (int i = tid; i < kSchedKeys; i += kSchedThreads) hist[i] = 0;
+  __threadfence_block();
+  __syncthreads();
   // 2: piece length S >= hkv * steps / kSplitTarget, so that the split pieces
   // (each kv-head counted) number at most 2 kSplitTarget and the items at most
   // kSplitTarget more than the tiles.
@@ -181,94 +180,52 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
   if (sl < kMinSplitSteps) sl = kMinSplitSteps;
   if (sl > (1 << 30)) sl = 1 << 30;
   const int S = (int)sl;
-
-  // 3: sequences by decreasing kv length (counting sort on 64-row units)
-  int* order = seqbuf;         // [batch] rank -> sequence
-  int* start = seqbuf + batch;  // [kWorkBuckets][batch] first position of (bucket, rank)
-  for (int b = tid; b < batch; b += kSchedThreads) {
-    const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
-    atomicAdd(&hist[kSchedKeys - 1 - clamp_key((s.k_len + 63) >> 6)], 1);
-  }
-  __syncthreads();
-  block_exclusive_scan(hist, kSchedKeys, wsum);
-  for (int b = tid; b < batch; b += kSchedThreads) {
-    const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
-    order[atomicAdd(&hist[kSchedKeys - 1 - clamp_key((s.k_len + 63) >> 6)], 1)] = b;
-  }
-  __threadfence_block();
-  __syncthreads();
-
-  // 4: item positions, a stable sort by (work bucket, heaviest first; sequence
-  // rank; piece; tile): the list stays close to longest-first, and the items of
-  // one bucket that sit side by side (one XCD's run) share a sequence and a
-  // piece index, i.e. they walk the same q blocks at the same time
-  for (int r = tid; r < batch; r += kSchedThreads) {
-    const SeqInfo s = seq_extent(cu_q, cu_k, order[r], total_q, total_k);
-    const int nt = (s.k_len + kBwdBN - 1) / kBwdBN;
-    int cnt[kWorkBuckets];
-#pragma unroll
-    for (int k = 0; k < kWorkBuckets; ++k) cnt[k] = 0;
-    for (int t = 0; t < nt; ++t) {
-      const int w = kv_tile_steps(s, t, causal, n_rep);
-      const int np = w > S ? (w + S - 1) / S : 1;
-      for (int pc = 0; pc < np; ++pc) {
-        const int bk = work_bucket(min(S, w - pc * S), S);
-#pragma unroll
-        for (int k = 0; k < kWorkBuckets; ++k) cnt[k] += k == bk;
-      }
+  // flattened tile i -> (sequence, tile): last b with tfirst[b] <= i
+  auto locate = [&](int i, int& b, int& t) {
+    int lo = 0, hi = batch - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tfirst[mid] <= i) lo = mid; else hi = mid - 1;
     }
-#pragma unroll
-    for (int k = 0; k < kWorkBuckets; ++k) start[k * batch + r] = cnt[k];
-  }
-  __threadfence_block();
-  __syncthreads();
-  const int total = scan_global(start, kWorkBuckets * batch, hist, wsum);
-
-  // 5: write the items; split tiles get consecutive partial slots and a
-  // SplitTile entry
-  for (int r = tid; r < batch; r += kSchedThreads) {
-    const int b = order[r];
+    b = lo;
+    t = i - tfirst[lo];
+  };
+  // 3: counting sort of the pieces by steps, heaviest first
+  for (int i = tid; i < ntiles; i += kSchedThreads) {
+    int b, t;
+    locate(i, b, t);
     const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
-    const int nt = (s.k_len + kBwdBN - 1) / kBwdBN;
-    int nsl = 0, maxnp = 1;
-    for (int t = 0; t < nt; ++t) {
-      const int w = kv_tile_steps(s, t, causal, n_rep);
-      const int np = w > S ? (w + S - 1) / S : 1;
-      if (np > 1) nsl += np;
-      maxnp = max(maxnp, np);
+    const int w = kv_tile_steps(s, t, causal, n_rep);
+    const int np = w > S ? (w + S - 1) / S : 1;
+    for (int pc = 0; pc < np; ++pc) atomicAdd(&hist[kSchedKeys - 1 - clamp_key(min(S, w - pc * S))], 1);
+  }
+  __syncthreads();
+  const int total = block_exclusive_scan(hist, kSchedKeys, wsum);
+  // 4: placement; split tiles get consecutive partial slots and a SplitTile entry
+  for (int i = tid; i < ntiles; i += kSchedThreads) {
+    int b, t;
+    locate(i, b, t);
+    const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
+    const int w = kv_tile_steps(s, t, causal, n_rep);
+    const int np = w > S ? (w + S - 1) / S : 1;
+    int slot0 = -1;
+    if (np > 1) {
+      slot0 = atomicAdd(&nslot, np);
+      const int k = atomicAdd(&nsplit_sh, 1);
+      if (k < kMaxSplitTiles) splits[k] = SplitTile{b, t, np, slot0};
     }
-    const int slot_base = nsl > 0 ? atomicAdd(&nslot, nsl) : 0;
-    int pos[kWorkBuckets];
-#pragma unroll
-    for (int k = 0; k < kWorkBuckets; ++k) pos[k] = start[k * batch + r];
-    for (int pc = 0; pc < maxnp; ++pc) {
-      int slot = slot_base;
-      for (int t = 0; t < nt; ++t) {
-        const int w = kv_tile_steps(s, t, causal, n_rep);
-        const int np = w > S ? (w + S - 1) / S : 1;
-        const int slot0 = np > 1 ? slot : -1;
-        if (np > 1) slot += np;
-        if (pc >= np) continue;
-        if (pc == 0 && np > 1) {
-          const int k = atomicAdd(&nsplit_sh, 1);
-          if (k < kMaxSplitTiles) splits[k] = SplitTile{b, t, np, slot0};
-        }
-        KvItem it;
-        it.b = b;
-        it.t = t;
-        it.s0 = pc * S;
-        it.s1 = min(w, (pc + 1) * S);
-        it.piece = pc;
-        it.np = np;
-        it.slot0 = slot0;
-        it.pad = 0;
-        const int bk = work_bucket(it.s1 - it.s0, S);
-        int at = 0;
-#pragma unroll
-        for (int k = 0; k < kWorkBuckets; ++k)
-          if (k == bk) at = pos[k]++;
-        if (at < kvcap) kvitems[at] = it;
-      }
+    for (int pc = 0; pc < np; ++pc) {
+      const int pos = atomicAdd(&hist[kSchedKeys - 1 - clamp_key(min(S, w - pc * S))], 1);
+      KvItem it;
+      it.b = b;
+      it.t = t;
+      it.s0 = pc * S;
+      it.s1 = min(w, (pc + 1) * S);
+      it.piece = pc;
+      it.np = np;
+      it.slot0 = slot0;
+      it.pad = 0;
+      if (pos < kvcap) kvitems[pos] = it;
     }
   }
   for (int i = total + tid; i < kvcap; i += kSchedThreads) {
