@@ -7,55 +7,33 @@
 //   dQ = scale * dS K,  dK = scale * dS^T Q.
 // P is recomputed from the forward's LSE: P = exp2(S * scale * log2e - LSE * log2e).
 //
-// Three kernels:
-//  * preprocess: Delta = rowsum(dO o O)                      (HBM-bound)
-//  * dK/dV: one workgroup = 8 waves = 128 kv rows of one kv-head.  Wave
-//    (g, kq) owns kv rows 32 kq .. 32 kq + 31 and q rows 32 g .. 32 g + 31 of
-//    each 64-row step, so every staged Q / dO tile feeds all 128 kv rows and
-//    every SIMD runs two waves.  K of the wave's rows sits in registers as the
-//    B operand of S = Q K^T, V in LDS as the B operand of dP = dO V^T.  A work
-//    item walks steps (q-head of the GQA group, q block) of its kv tile, with
-//    Q / dO / LSE2 / Delta triple-buffered in LDS by direct global->LDS loads
-//    (two steps in flight); dV^T += dO^T P and dK^T += Q^T dS read dO^T / Q^T
-//    with ds_read_b64_tr_b16.  The two q-group waves' partial dK/dV of each kv
-//    quarter are summed through LDS.  Tiles heavier than the scheduler's
-//    piece length run as several work items writing fp32 sums to workspace
-//    slots, which a small kernel adds in piece order afterwards.
+// Kernels, in launch order:
 //  * dQ: one workgroup = 4 waves = 128 q rows of one q-head (same schedule as
 //    the forward); wave g owns q rows 32 g .. 32 g + 31 with Q and dO in
-//    registers as B operands of S^T = K Q^T and dP^T = V dO^T.  K and V tiles
+//    registers as B operands of S^T = K Q^T and dP^T = V dO^T.  Each lane
+//    also reads its row's O to form Delta = rowsum(dO o O), and the kernel
+//    publishes Delta and LSE * log2(e) for the dK/dV kernel.  K and V tiles
 //    of 64 rows are double-buffered row-major in LDS and taken 32 rows at a
 //    time (operand reads one k-step ahead of the MFMAs); dQ^T += K^T dS^T reads
 //    K^T with ds_read_b64_tr_b16.
+//  * dK/dV: one workgroup = 8 waves = 128 kv rows of one kv-head.  Wave
+//    (g, kq) owns kv rows 32 kq .. 32 kq + 31 and q rows 32 g .. 32 g + 31 of
+//    each 64-row step, so every staged Q / dO tile feeds all 128 kv rows and
+//    every SIMD runs two waves.  K and V of the tile sit in LDS as the B
+//    operands of S = Q K^T and dP = dO V^T.  A work item walks steps (q block,
+//    q-head of the GQA group) of its kv tile, with Q / dO / LSE2 / Delta
+//    double-buffered in LDS by direct global->LDS loads and the operand reads
+//    one k-step ahead of the MFMAs; dV^T += dO^T P and dK^T += Q^T dS read
+//    dO^T / Q^T with ds_read_b64_tr_b16.  The two q-group waves' partial
+//    dK/dV of each kv quarter are summed through LDS.  Tiles heavier than the
+//    scheduler's piece length run as several work items writing fp32 sums to
+//    workspace slots,
+//  * which the partial-sum kernel adds in piece order afterwards.
 #include "attn.h"
 
 namespace siq {
 
 namespace {
-
-template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_preprocess_kernel(const AttnParams p) {
-  constexpr int TPR = D / 8;         // threads per (token, head) row
-  constexpr int RPB = 256 / TPR;     // rows per block iteration
-  const int tid = threadIdx.x, sub = tid % TPR;
-  const int64_t nrows = p.total_q * p.hq;
-  for (int64_t row = (int64_t)blockIdx.x * RPB + tid / TPR; row < nrows; row += (int64_t)gridDim.x * RPB) {
-    const int64_t t = row / p.hq;
-    const int hh = (int)(row - t * p.hq);
-    const bf16x8 o = ld_bf16x8(p.o + t * p.o_tok + hh * p.o_head + 8 * sub);
-    const bf16x8 g = ld_bf16x8(p.dout + t * p.do_tok + hh * p.do_head + 8 * sub);
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc += (float)o[i] * (float)g[i];
-#pragma unroll
-    for (int m = TPR / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
-    if (sub == 0) {
-      const int64_t idx = (int64_t)hh * p.lse_head + t;
-      p.delta[idx] = acc;
-      p.lse2[idx] = p.lse[idx] * kLog2e;
-    }
-  }
-}
 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams p) {
@@ -359,19 +337,31 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
   bf16x8 qf[D / 16], gf[D / 16];
   float lse2, dlt;
   {
+    // Q and dO of this lane's row (half h of its d), and the row's
+    // Delta = rowsum(dO o O) and LSE * log2(e), which this kernel also
+    // publishes for the dK/dV kernel that runs after it
     const int64_t r = si.q_start + (qvalid ? qrow : 0);
     const bf16* qp = p.q + r * p.q_tok + (int64_t)hqi * p.q_head + 8 * h;
     const bf16* gp = p.dout + r * p.do_tok + (int64_t)hqi * p.do_head + 8 * h;
+    const bf16* op = p.o + r * p.o_tok + (int64_t)hqi * p.o_head + 8 * h;
+    float acc = 0.f;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
-      const bf16x8 a = ld_bf16x8(qp + 16 * ks), b = ld_bf16x8(gp + 16 * ks);
+      const bf16x8 a = ld_bf16x8(qp + 16 * ks), b = ld_bf16x8(gp + 16 * ks), o = ld_bf16x8(op + 16 * ks);
       qf[ks] = qvalid ? a : zero_bf16x8();
       gf[ks] = qvalid ? b : zero_bf16x8();
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = __builtin_fmaf((float)b[i], (float)o[i], acc);
     }
+    acc += __shfl_xor(acc, 32);
     const int64_t idx = (int64_t)hqi * p.lse_head + r;
-    const float l2 = p.lse2[idx], dl = p.delta[idx];
+    const float l2 = p.lse[idx] * kLog2e;
+    if (qvalid && h == 0) {
+      p.delta[idx] = acc;
+      p.lse2[idx] = l2;
+    }
     lse2 = qvalid ? l2 : INFINITY;
-    dlt = qvalid ? dl : 0.f;
+    dlt = qvalid ? acc : 0.f;
   }
   f32x16 dq[NDT];
 #pragma unroll
@@ -460,17 +450,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
 
 template <int D, bool CAUSAL>
 hipError_t launch_bwd_t(const AttnParams& p, int qcap, int kvcap, hipStream_t stream) {
-  const int64_t rows = p.total_q * p.hq;
-  if (rows > 0) {
-    const int rpb = 256 / (D / 8);
-    int64_t blocks = (rows + rpb - 1) / rpb;
-    if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL((attn_bwd_preprocess_kernel<D>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
-  }
+  // dQ first: it also writes Delta and LSE2, which the dK/dV kernel reads
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)qcap * p.hq)), dim3(256), 0, stream, p);
   hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)kvcap * p.hkv)), dim3(512), 0, stream,
                      p);
   hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D>), dim3(kMaxSplitTiles, p.hkv), dim3(256), 0, stream, p);
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)qcap * p.hq)), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
