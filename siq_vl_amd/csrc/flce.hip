@@ -56,6 +56,23 @@ struct GOp {
 __device__ __forceinline__ int swz_kc(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
 __device__ __forceinline__ int swz_nkc(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
+// One wave instruction of direct global->LDS loading: lane l's 16 bytes land
+// at LDS byte lds + 16 l.  Written as inline asm so that the compiler's wait
+// insertion does not track these loads: it cannot tell the slab being read
+// from the one being loaded (both live in one LDS array) and would wait for
+// the prefetch before the first transposed read of every step.  The GEMM loop
+// orders them with the LDS reads itself (wait_vmem, then a barrier).  The LDS
+// address goes in m0, which needs one wait state after its write.
+__device__ __forceinline__ void dma16(const bf16* gbase, uint32_t elem_off, const bf16* lds) {
+  const uint32_t la = (uint32_t)(uintptr_t)(lds_void*)lds;
+  const uint32_t byte_off = elem_off << 1;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(byte_off), "s"(gbase), "{m0}"(la) : "memory");
+}
+__device__ __forceinline__ void dma16(const bf16* gptr, const bf16* lds) {
+  const uint32_t la = (uint32_t)(uintptr_t)(lds_void*)lds;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "{m0}"(la) : "memory");
+}
+
 // Direct global->LDS staging of one slab: 32 instructions of 1 KB, 8 per wave.
 // Rows / chunks past the operand's extent re-read the last valid one (always in
 // bounds); the garbage that produces is either never stored (M/N tails) or
@@ -96,7 +113,7 @@ struct SlabLoad {
           const int r = wrow + 2 * k + lrow;
           o = (uint32_t)(r * op.ld + 8 * (lpc ^ swz_nkc(r)));
         }
-        __builtin_amdgcn_global_load_lds(base + o, (lds_void*)(lds + (wu * PERW + k) * 512), 16, 0, 0);
+        dma16(base, o, lds + (wu * PERW + k) * 512);
       }
       return;
     }
@@ -108,8 +125,7 @@ struct SlabLoad {
       int64_t gc = KC ? k0 + 8 * c : r0 + 8 * c;
       gr = gr < op.rows ? gr : op.rows - 1;
       gc = gc < op.cols ? gc : op.cols - 8;
-      __builtin_amdgcn_global_load_lds(op.base + gr * op.ld + gc, (lds_void*)(lds + (wu * PERW + k) * 512), 16,
-                                       0, 0);
+      dma16(op.base + gr * op.ld + gc, lds + (wu * PERW + k) * 512);
     }
   }
 };
@@ -169,32 +185,46 @@ struct DzForm {
   int64_t nvt, nc, vocab;
 };
 
+// The per-row scalars of the slab a thread applies dZ to, loaded one step
+// before the pass so that their latency hides behind the MFMAs (kept raw: the
+// offsets derived from them are formed in the pass).
+struct DzRow {
+  float fv, gv;
+  int64_t y;      // label of the row's token
+  int64_t vbase;  // vocabulary index of the slab row's first column
+  bool valid;     // the token row lies inside the chunk (else dZ = 0)
+};
+
 // Each of the 512 threads owns 4 chunks of one token row; the chunk visited at
 // step k is staggered by row so that every quarter-wave touches 16 distinct
 // bank groups.
 template <bool KC>
-__device__ __forceinline__ void dz_pass(const DzForm& F, bf16* S, int64_t j0, int64_t k0, int tid) {
-  int r, q;
-  int64_t tok, vbase;
-  if (KC) {  // [256 tok][64 v] (8 chunks / row): J = tok, k = v
-    r = tid >> 1;
-    q = tid & 1;
-    tok = j0 + r;
-    vbase = k0;
-  } else {   // [64 tok][256 v] (32 chunks / row): k = tok, J = v
-    r = tid >> 3;
-    q = tid & 7;
-    tok = k0 + r;
-    vbase = j0;
-  }
+__device__ __forceinline__ DzRow dz_load(const DzForm& F, int64_t j0, int64_t k0, int tid) {
+  // KC: [256 tok][64 v] (8 chunks / row), J = tok, k = v;
+  // NKC: [64 tok][256 v] (32 chunks / row), k = tok, J = v
+  const int r = KC ? tid >> 1 : tid >> 3;
+  const int64_t tok = KC ? j0 + r : k0 + r;
   const bool tv = tok < F.nc;
+  const int64_t t = tv ? tok : 0;
   const int64_t tile = (KC ? k0 : j0) / kVT;
-  const float fv = tv ? F.f[tok * F.nvt + tile] : 0.f;
-  const float gv = tv ? F.g[tok] : 0.f;
-  // label and vocabulary end relative to this row's first column (32-bit)
-  const int64_t yrel64 = tv ? F.y[tok] - vbase : -1;
+  DzRow d;
+  d.fv = F.f[t * F.nvt + tile];
+  d.gv = F.g[t];
+  d.y = F.y[t];
+  d.vbase = KC ? k0 : j0;
+  d.valid = tv;
+  return d;
+}
+
+template <bool KC>
+__device__ __forceinline__ void dz_pass(const DzRow& d, int64_t vocab, bf16* S, int tid) {
+  const int r = KC ? tid >> 1 : tid >> 3, q = KC ? tid & 1 : tid & 7;
+  const float fv = d.valid ? d.fv : 0.f, gv = d.valid ? d.gv : 0.f;
+  // label and vocabulary end relative to this row's first column (32-bit); a
+  // row past the chunk has gv = 0, so its label never matters
+  const int64_t yrel64 = d.y - d.vbase;
   const int yrel = (yrel64 >= 0 && yrel64 < 256) ? (int)yrel64 : -1;
-  const int64_t vend64 = F.vocab - vbase;
+  const int64_t vend64 = vocab - d.vbase;
   const int vend = vend64 > 256 ? 256 : (int)vend64;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -266,7 +296,7 @@ __device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B
   wait_vmem();
   __syncthreads();
   if (BFORM && nk > 0) {
-    dz_pass<BKC>(form, smem + SLAB, j0, kb, tid);
+    dz_pass<BKC>(dz_load<BKC>(form, j0, kb, tid), form.vocab, smem + SLAB, tid);
     __syncthreads();
   }
   for (int it = 0; it < nk; ++it) {
@@ -275,9 +305,11 @@ __device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B
     const bool more = it + 1 < nk;
     bf16* nx = smem + ((it + 1) & 1) * 2 * SLAB;
     const int64_t kn = kb + (int64_t)(it + 1) * BK;
+    DzRow dn{};
     if (more) {
       la.issue(A, i0, kn, nx, wu);
       lb.issue(B, j0, kn, nx + SLAB, wu);
+      if (BFORM) dn = dz_load<BKC>(form, j0, kn, tid);
     }
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
@@ -294,7 +326,7 @@ __device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B
     wait_vmem();
     __syncthreads();
     if (BFORM && more) {
-      dz_pass<BKC>(form, nx + SLAB, j0, kn, tid);
+      dz_pass<BKC>(dn, form.vocab, nx + SLAB, tid);
       __syncthreads();
     }
   }
