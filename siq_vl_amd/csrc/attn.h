@@ -8,7 +8,7 @@
 namespace siq {
 
 // Tile sizes shared by the scheduler and the kernels.
-constexpr int kFwdBM = 128;    // q rows per forward / dQ workgroup (4 waves x 32)
+constexpr int kFwdBM = 128;    // q rows per forward unit (4 waves x 32) and per dQ workgroup
 constexpr int kFwdBN = 64;     // kv rows per inner step of the forward / dQ loop
 constexpr int kBwdBN = 128;    // kv rows per dK/dV work item (4 quarters of 32)
 constexpr int kBwdBM = 64;     // q rows per step of the dK/dV loop (2 groups of 32)
@@ -82,8 +82,9 @@ inline int64_t tile_cap(int64_t total, int batch, int rows) { return total / row
 inline int64_t kv_item_cap(int64_t total_k, int batch) { return tile_cap(total_k, batch, kBwdBN) + kSplitTarget + 1; }
 
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,
-                           int causal, int n_rep, int hkv, SeqInfo* seq, int2* qtiles, int qcap, KvItem* kvitems,
-                           int kvcap, int* seqbuf, SplitTile* splits, int* nsplit, hipStream_t stream);
+                           int causal, int n_rep, int hkv, SeqInfo* seq, int2* qtiles, int qrows, int qcap,
+                           KvItem* kvitems, int kvcap, int* seqbuf, SplitTile* splits, int* nsplit,
+                           hipStream_t stream);
 hipError_t launch_attn_fwd(const AttnParams& p, int d, int causal, int qcap, hipStream_t stream);
 hipError_t launch_attn_bwd(const AttnParams& p, int d, int causal, int qcap, int kvcap, hipStream_t stream);
 

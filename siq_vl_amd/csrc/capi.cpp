@@ -161,8 +161,8 @@ int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, fl
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0, hq / hkv, hkv,
                                       reinterpret_cast<siq::SeqInfo*>(base + L.seq),
-                                      reinterpret_cast<int2*>(base + L.qtiles), L.qcap, nullptr, 0, nullptr,
-                                      nullptr, nullptr, s);
+                                      reinterpret_cast<int2*>(base + L.qtiles), siq::kFwdBM, L.qcap, nullptr, 0,
+                                      nullptr, nullptr, nullptr, s);
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
   e = siq::launch_attn_fwd(p, d, causal != 0, L.qcap, s);
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "attention forward launch failed: %s", hipGetErrorString(e));
@@ -237,7 +237,7 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0, hq / hkv, hkv,
                                       reinterpret_cast<siq::SeqInfo*>(base + L.seq),
-                                      reinterpret_cast<int2*>(base + L.qtiles), L.qcap,
+                                      reinterpret_cast<int2*>(base + L.qtiles), siq::kFwdBM, L.qcap,
                                       reinterpret_cast<siq::KvItem*>(base + L.kvitems), L.kvcap,
                                       reinterpret_cast<int*>(base + L.seqbuf),
                                       reinterpret_cast<siq::SplitTile*>(base + L.splits),

@@ -8,8 +8,8 @@
 // out of bounds, and writes the work lists ordered by decreasing work with a
 // counting sort.  The attention kernels then map blockIdx.x -> work.
 //
-// Block 0 builds the q-tile list of the forward and dQ kernels, heaviest
-// first (work key: kv rows seen, in units of 64).  Block 1 builds the dK/dV
+// Block 0 builds the q-tile list of the forward and dQ kernels (tiles of
+// `qrows` rows), heaviest first (work key: kv rows seen, in units of 64).  Block 1 builds the dK/dV
 // work items: a kv tile has n_rep x (q blocks that can see it) steps; tiles
 // with more than S = max(kMinSplitSteps, hkv total / kSplitTarget) steps are
 // cut into pieces of at most S steps, so that the longest item stays near the
@@ -36,12 +36,12 @@ __device__ __forceinline__ SeqInfo seq_extent(const int* cu_q, const int* cu_k, 
   return s;
 }
 
-// kv rows that q tile t sees (causal alignment is bottom-right: q row i sees
-// k rows <= i + (Lk - Lq)), in units of 64.
-__device__ __forceinline__ int q_tile_key(const SeqInfo& s, int t, int causal) {
+// kv rows that q tile t of `rows` rows sees (causal alignment is
+// bottom-right: q row i sees k rows <= i + (Lk - Lq)), in units of 64.
+__device__ __forceinline__ int q_tile_key(const SeqInfo& s, int t, int rows, int causal) {
   const int off = s.k_len - s.q_len;
   int n = s.k_len;
-  if (causal) n = max(0, min(s.k_len, (t + 1) * kFwdBM + off));
+  if (causal) n = max(0, min(s.k_len, (t + 1) * rows + off));
   const int key = (n + 63) >> 6;
   return key < kSchedKeys - 1 ? key : kSchedKeys - 1;
 }
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
                                                                  const int* __restrict__ cu_k, int batch,
                                                                  int64_t total_q, int64_t total_k, int causal,
                                                                  int n_rep, int hkv, SeqInfo* __restrict__ seq,
-                                                                 int2* __restrict__ qtiles, int qcap,
+                                                                 int2* __restrict__ qtiles, int qrows, int qcap,
                                                                  KvItem* __restrict__ kvitems, int kvcap,
                                                                  int* __restrict__ seqbuf,
                                                                  SplitTile* __restrict__ splits,
@@ -134,16 +134,16 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
     for (int b = tid; b < batch; b += kSchedThreads) {
       const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
       seq[b] = s;
-      const int nt = (s.q_len + kFwdBM - 1) / kFwdBM;
-      for (int t = 0; t < nt; ++t) atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(s, t, causal)], 1);
+      const int nt = (s.q_len + qrows - 1) / qrows;
+      for (int t = 0; t < nt; ++t) atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(s, t, qrows, causal)], 1);
     }
     __syncthreads();
     const int total = block_exclusive_scan(hist, kSchedKeys, wsum);
     for (int b = tid; b < batch; b += kSchedThreads) {
       const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
-      const int nt = (s.q_len + kFwdBM - 1) / kFwdBM;
+      const int nt = (s.q_len + qrows - 1) / qrows;
       for (int t = 0; t < nt; ++t) {
-        const int pos = atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(s, t, causal)], 1);
+        const int pos = atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(s, t, qrows, causal)], 1);
         if (pos < qcap) qtiles[pos] = make_int2(b, t);
       }
     }
@@ -240,11 +240,12 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
 }  // namespace
 
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,
-                           int causal, int n_rep, int hkv, SeqInfo* seq, int2* qtiles, int qcap, KvItem* kvitems,
-                           int kvcap, int* seqbuf, SplitTile* splits, int* nsplit, hipStream_t stream) {
+                           int causal, int n_rep, int hkv, SeqInfo* seq, int2* qtiles, int qrows, int qcap,
+                           KvItem* kvitems, int kvcap, int* seqbuf, SplitTile* splits, int* nsplit,
+                           hipStream_t stream) {
   const int blocks = kvitems != nullptr ? 2 : 1;
   hipLaunchKernelGGL(schedule_kernel, dim3(blocks), dim3(kSchedThreads), 0, stream, cu_q, cu_k, batch, total_q,
-                     total_k, causal, n_rep, hkv, seq, qtiles, qcap, kvitems, kvcap, seqbuf, splits, nsplit);
+                     total_k, causal, n_rep, hkv, seq, qtiles, qrows, qcap, kvitems, kvcap, seqbuf, splits, nsplit);
   return hipGetLastError();
 }
 

@@ -39,9 +39,9 @@ __device__ __forceinline__ int wave_uniform(int x) { return __builtin_amdgcn_rea
 // issues instructions w*PERW .. w*PERW + PERW - 1; instruction i covers rows
 // [i*RPI, (i+1)*RPI) (1 KB, 64 chunks), lane l taking row i*RPI + l / CH and
 // chunk position l % CH.  The swizzle repeats every 16 rows, so a lane only
-// keeps PAT = 16 / RPI base offsets; the rest is a uniform row shift.  Rows
-// >= nrows load the last valid row instead (always in bounds; consumers mask
-// those rows or multiply them by exact zeros).
+// keeps PAT = 16 / RPI chunk offsets.  Rows >= nrows load the last valid row
+// instead (always in bounds; consumers mask those rows or multiply them by
+// exact zeros).
 template <int ROWS, int D, int NW>
 struct LdsTile {
   static constexpr int CH = D / 8;
@@ -52,34 +52,43 @@ struct LdsTile {
   static constexpr int ELEMS = ROWS * D;
   static_assert(NINSTR % NW == 0 && PERW % PAT == 0, "tile splits evenly over the waves");
 
-  uint32_t base[PAT];  // element offset of this lane's chunk for instruction p (p < PAT), row shift excluded
+  uint32_t coff[PAT];  // element offset of this lane's chunk inside its row, for instruction p (p < PAT)
   int lrow;            // row of this lane inside an instruction
 
   __device__ __forceinline__ void init(int64_t stride, int lane) {
+    (void)stride;
     lrow = lane / CH;
     const int pc = lane % CH;
 #pragma unroll
-    for (int pi = 0; pi < PAT; ++pi) {
-      const int r = pi * RPI + lrow;
-      base[pi] = (uint32_t)(r * stride + 8 * (pc ^ swz<D>(r)));
-    }
+    for (int pi = 0; pi < PAT; ++pi) coff[pi] = (uint32_t)(8 * (pc ^ swz<D>(pi * RPI + lrow)));
   }
 
   // gbase: (row 0, col 0) of the tile in global memory; lds: the tile's LDS
-  // base; wu: this wave's index (wave-uniform).
+  // base; wu: this wave's index among the NW staging waves (wave-uniform).
+  // Offsets are 32-bit element counts from gbase (a tile spans < 2^31 elements).
+  //
+  // UNTRACKED = true issues the loads through inline asm, hidden from the
+  // compiler's wait insertion: it cannot tell the ring slot being filled from
+  // the ones being read and would wait for every prefetch before the next LDS
+  // read.  The caller then orders them itself (wait_vmcnt, then a barrier).
+  template <bool UNTRACKED = false>
   __device__ __forceinline__ void issue(const bf16* gbase, int64_t stride, int nrows, bf16* lds, int wu) const {
+    const uint32_t st = (uint32_t)stride;
 #pragma unroll
     for (int k = 0; k < PERW; ++k) {
       const int i = wu * PERW + k;
-      const int r0 = (i - (k % PAT)) * RPI;  // uniform row shift (multiple of 16)
-      uint32_t o = base[k % PAT] + (uint32_t)(r0 * stride);
-      if (nrows < ROWS) {
-        const int r = i * RPI + lrow;
-        o = r < nrows ? o : o - (uint32_t)((r - nrows + 1) * stride);
+      int r = i * RPI + lrow;
+      if (nrows < ROWS) r = min(r, nrows - 1);
+      const uint32_t o = (uint32_t)r * st + coff[k % PAT];
+      if constexpr (UNTRACKED) {
+        // lane l's 16 bytes land at LDS byte m0 + 16 l; m0 needs one wait state after its write
+        const uint32_t la = (uint32_t)(uintptr_t)(lds_void*)(lds + i * 512);
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(o << 1), "s"(gbase), "{m0}"(la) : "memory");
+      } else {
+        // uniform base + 32-bit byte offset: the saddr + voffset form
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(gbase) + (o << 1), (lds_void*)(lds + i * 512),
+                                         16, 0, 0);
       }
-      // uniform base + 32-bit byte offset: the saddr + voffset form
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(gbase) + (o << 1), (lds_void*)(lds + i * 512),
-                                       16, 0, 0);
     }
   }
 };
@@ -140,6 +149,9 @@ struct TrRead {
 
 // Wait for this wave's outstanding global (and direct-to-LDS) loads.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Wait for this wave's outstanding LDS reads (lgkmcnt(0), vmcnt untouched).
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // Wait until at most N of this wave's global loads are outstanding (loads
 // complete in issue order, so everything but the newest N has landed).
