@@ -62,11 +62,16 @@ __device__ __forceinline__ int swz_nkc(int r) { return ((r & 3) << 2) | ((r >> 2
 // from the one being loaded (both live in one LDS array) and would wait for
 // the prefetch before the first transposed read of every step.  The GEMM loop
 // orders them with the LDS reads itself (wait_vmem, then a barrier).  The LDS
-// address goes in m0, which needs one wait state after its write.
+// address goes in m0 (one wait state after its write) and the uniform base in
+// SGPRs, which the compiler may have just written from a VALU instruction
+// (v_readfirstlane; an SGPR written by VALU and read by VMEM needs five wait
+// states): its hazard checks do not look inside the asm, so it starts with
+// s_nop 4.
 __device__ __forceinline__ void dma16(const bf16* gbase, uint32_t elem_off, const bf16* lds) {
   const uint32_t la = (uint32_t)(uintptr_t)(lds_void*)lds;
   const uint32_t byte_off = elem_off << 1;
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(byte_off), "s"(gbase), "{m0}"(la) : "memory");
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(byte_off), "s"(gbase), "{m0}"(la)
+               : "memory");
 }
 __device__ __forceinline__ void dma16(const bf16* gptr, const bf16* lds) {
   const uint32_t la = (uint32_t)(uintptr_t)(lds_void*)lds;

@@ -81,9 +81,12 @@ struct LdsTile {
       if (nrows < ROWS) r = min(r, nrows - 1);
       const uint32_t o = (uint32_t)r * st + coff[k % PAT];
       if constexpr (UNTRACKED) {
-        // lane l's 16 bytes land at LDS byte m0 + 16 l; m0 needs one wait state after its write
+        // lane l's 16 bytes land at LDS byte m0 + 16 l.  s_nop 4: m0 needs one wait state after its
+        // write, and the base SGPRs may have been written by a VALU instruction (an SGPR written by
+        // VALU and read by VMEM needs five), which the compiler's hazard checks do not see in asm.
         const uint32_t la = (uint32_t)(uintptr_t)(lds_void*)(lds + i * 512);
-        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(o << 1), "s"(gbase), "{m0}"(la) : "memory");
+        asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(o << 1), "s"(gbase), "{m0}"(la)
+                     : "memory");
       } else {
         // uniform base + 32-bit byte offset: the saddr + voffset form
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(gbase) + (o << 1), (lds_void*)(lds + i * 512),
