@@ -15,11 +15,12 @@
 //     max m and the sum s of exp(z - m) (the chunked-vocab logsumexp), the
 //     label logit z_y, and E = exp(z - m) in bf16 (a value in (0, 1], so bf16
 //     keeps full relative precision however large the logits are).
-//  2. row reduce: lse = M + log(sum_t s_t exp(m_t - M)); per tile the factor
-//     f = exp(m_t - lse) * g (g = inv_den or 0), so that dZ = E * f - g * [v == y].
+//  2. row pass: lse = M + log(sum_t s_t exp(m_t - M)), the row's loss, and E
+//     rewritten in place as dZ = E * f_t - g * [v == y] with f_t = exp(m_t -
+//     lse) * g (g = inv_den, or 0 for an ignored row): one multiply per element,
+//     once for both gradient GEMMs.
 //  3. dH GEMM  dH_c^T = W^T dZ_c^T (split over the vocab) and
-//  4. dW GEMM  dW^T = H_c^T dZ_c, both forming dZ from E on the fly while
-//     staging it into LDS (one multiply per element; no exp in the GEMMs).
+//  4. dW GEMM  dW^T = H_c^T dZ_c.
 // With several chunks dW accumulates in an fp32 workspace.  Every reduction
 // has a fixed order, so results are bitwise reproducible.
 #include "flce.h"
@@ -179,77 +180,29 @@ struct SlabRead {
 
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// dZ from the exp-normalised logits chunk E, applied to a B slab in LDS after
-// it lands: dZ = E * f[tok, tile] - g[tok] * [v == y[tok]], zero for token rows
-// past the chunk and vocab columns past V.  Each thread owns one token row of
-// the slab (KC: a whole 64-column row; NKC: a quarter of a 256-column row).
-struct DzForm {
-  const float* f;        // [C, nvt]
-  const float* g;        // [C]
-  const int64_t* y;      // [C] labels of the chunk
-  int64_t nvt, nc, vocab;
-};
-
-// The per-row scalars of the slab a thread applies dZ to, loaded one step
-// before the pass so that their latency hides behind the MFMAs (kept raw: the
-// offsets derived from them are formed in the pass).
-struct DzRow {
-  float fv, gv;
-  int64_t y;      // label of the row's token
-  int64_t vbase;  // vocabulary index of the slab row's first column
-  bool valid;     // the token row lies inside the chunk (else dZ = 0)
-};
-
-// Each of the 512 threads owns 4 chunks of one token row; the chunk visited at
-// step k is staggered by row so that every quarter-wave touches 16 distinct
-// bank groups.
+// Zeroes the K tail of a B slab (k >= kval) after it lands, for the last,
+// partial k-step: the slab loader fills those rows / chunks by re-reading the
+// last valid one, and the product must not see them.  KC [256][64]: thread t
+// owns row t / 2, logical chunks 4 (t % 2) .. +3; NKC [64][256]: row t / 8,
+// chunks 4 (t % 8) .. +3.
 template <bool KC>
-__device__ __forceinline__ DzRow dz_load(const DzForm& F, int64_t j0, int64_t k0, int tid) {
-  // KC: [256 tok][64 v] (8 chunks / row), J = tok, k = v;
-  // NKC: [64 tok][256 v] (32 chunks / row), k = tok, J = v
+__device__ __forceinline__ void ztail_pass(bf16* S, int kval, int tid) {
   const int r = KC ? tid >> 1 : tid >> 3;
-  const int64_t tok = KC ? j0 + r : k0 + r;
-  const bool tv = tok < F.nc;
-  const int64_t t = tv ? tok : 0;
-  const int64_t tile = (KC ? k0 : j0) / kVT;
-  DzRow d;
-  d.fv = F.f[t * F.nvt + tile];
-  d.gv = F.g[t];
-  d.y = F.y[t];
-  d.vbase = KC ? k0 : j0;
-  d.valid = tv;
-  return d;
-}
-
-template <bool KC>
-__device__ __forceinline__ void dz_pass(const DzRow& d, int64_t vocab, bf16* S, int tid) {
-  const int r = KC ? tid >> 1 : tid >> 3, q = KC ? tid & 1 : tid & 7;
-  const float fv = d.valid ? d.fv : 0.f, gv = d.valid ? d.gv : 0.f;
-  // label and vocabulary end relative to this row's first column (32-bit); a
-  // row past the chunk has gv = 0, so its label never matters
-  const int64_t yrel64 = d.y - d.vbase;
-  const int yrel = (yrel64 >= 0 && yrel64 < 256) ? (int)yrel64 : -1;
-  const int64_t vend64 = vocab - d.vbase;
-  const int vend = vend64 > 256 ? 256 : (int)vend64;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int pc = KC ? 4 * q + ((k + (r >> 1)) & 3) : 4 * q + ((k + r + 2 * (q >> 2)) & 3);
-    const int c = KC ? (pc ^ swz_kc(r)) : (pc ^ swz_nkc(r));
+    const int c = KC ? 4 * (tid & 1) + k : 4 * (tid & 7) + k;
+    const int pc = KC ? (c ^ swz_kc(r)) : (c ^ swz_nkc(r));
     bf16* ptr = S + (KC ? r * BK : r * 256) + pc * 8;
-    const bf16x8 e = ld_bf16x8(ptr);
-    bf16x8 o;
+    if (KC) {
+      if (8 * c + 8 > kval) {
+        bf16x8 x = ld_bf16x8(ptr);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (bf16)((float)e[i] * fv);
-    const int cb = 8 * c;
-    if (yrel - cb >= 0 && yrel - cb < 8) {  // the label column (one chunk per valid row)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (i == yrel - cb) ? (bf16)((float)e[i] * fv - gv) : o[i];
+        for (int i = 0; i < 8; ++i) x[i] = 8 * c + i < kval ? x[i] : (bf16)0.f;
+        st_bf16x8(ptr, x);
+      }
+    } else if (r >= kval) {
+      st_bf16x8(ptr, zero_bf16x8());
     }
-    if (cb + 8 > vend) {  // columns past the vocabulary (last tile only)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = cb + i < vend ? o[i] : (bf16)0.f;
-    }
-    st_bf16x8(ptr, o);
   }
 }
 
@@ -273,11 +226,11 @@ __device__ __forceinline__ bool tile_of(int nI, int nJ, int GI, int& ti, int& tj
 // C[i][j] = sum_k A[i][k] B[j][k] over k in [kb, ke) (kb, ke multiples of BK
 // except ke at the operand's end) with 8 waves of 128x64 (4x2 MFMA 32x32
 // tiles; two waves per SIMD).  acc[ti][tj][r] holds
-// i = i0 + 128*wi + 32*ti + drow(r, h), j = j0 + 64*wj + 32*tj + l32.  With
-// BFORM the B slab is turned into dZ in LDS after it lands.
-template <bool AKC, bool BKC, bool BFORM>
-__device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B, const DzForm& form, int64_t i0,
-                                          int64_t j0, int64_t kb, int64_t ke, f32x16 (&acc)[4][2]) {
+// i = i0 + 128*wi + 32*ti + drow(r, h), j = j0 + 64*wj + 32*tj + l32.  A
+// last k-step that ends past ke has its B slab's tail zeroed (ztail_pass).
+template <bool AKC, bool BKC>
+__device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B, int64_t i0, int64_t j0, int64_t kb,
+                                          int64_t ke, f32x16 (&acc)[4][2]) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wi = w & 1, wj = w >> 1;
   const int wu = __builtin_amdgcn_readfirstlane(w);
@@ -300,21 +253,24 @@ __device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B
   }
   wait_vmem();
   __syncthreads();
-  if (BFORM && nk > 0) {
-    dz_pass<BKC>(dz_load<BKC>(form, j0, kb, tid), form.vocab, smem + SLAB, tid);
-    __syncthreads();
-  }
+  // the B slab of k-step s, once landed: zero its tail if the step ends past ke
+  auto ztail = [&](int s, bf16* Bslab) {
+    const int64_t k0 = kb + (int64_t)s * BK;
+    if (k0 + BK > ke) {
+      ztail_pass<BKC>(Bslab, (int)(ke - k0), tid);
+      __syncthreads();
+    }
+  };
+  if (nk > 0) ztail(0, smem + SLAB);
   for (int it = 0; it < nk; ++it) {
     const bf16* As = smem + (it & 1) * 2 * SLAB;
     const bf16* Bs = As + SLAB;
     const bool more = it + 1 < nk;
     bf16* nx = smem + ((it + 1) & 1) * 2 * SLAB;
     const int64_t kn = kb + (int64_t)(it + 1) * BK;
-    DzRow dn{};
     if (more) {
       la.issue(A, i0, kn, nx, wu);
       lb.issue(B, j0, kn, nx + SLAB, wu);
-      if (BFORM) dn = dz_load<BKC>(form, j0, kn, tid);
     }
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
@@ -330,10 +286,7 @@ __device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B
     }
     wait_vmem();
     __syncthreads();
-    if (BFORM && more) {
-      dz_pass<BKC>(dn, form.vocab, nx + SLAB, tid);
-      __syncthreads();
-    }
+    if (more) ztail(it + 1, nx + SLAB);
   }
 }
 
@@ -355,8 +308,7 @@ __global__ __launch_bounds__(NT) void flce_logits_kernel(const LogitsArgs p) {
   if (!tile_of(p.nI, p.nJ, 4, ti, tj)) return;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
   f32x16 acc[4][2];
-  DzForm none{};
-  gemm_core<true, true, false>(smem, p.W, p.H, none, i0, j0, 0, p.W.cols, acc);
+  gemm_core<true, true>(smem, p.W, p.H, i0, j0, 0, p.W.cols, acc);
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int wi = w & 1, wj = w >> 1;
@@ -425,23 +377,26 @@ __global__ __launch_bounds__(NT) void flce_logits_kernel(const LogitsArgs p) {
   }
 }
 
-// ---------------------------------------------------------------- row reduce
-struct ReduceArgs {
-  float* mpart;  // in: tile max; out: f = exp2(m - lse2) * g
-  const float* spart;
+// ---------------------------------------------------------------- row pass
+struct RowArgs {
+  const float* mpart;    // [nc, nvt] tile max (log2 units)
+  const float* spart;    // [nc, nvt] tile sum of exp2(z2 - m)
   const float* zy;
   const int64_t* y;      // chunk labels
-  float* g;              // [nc]
+  bf16* E;               // [nc, V]: E on entry, dZ on exit
   float* loss_row;       // [nc] (chunk slice)
   const float* invden;
   int64_t nc, nvt, V, ignore_index;
 };
 
-__global__ __launch_bounds__(256) void flce_reduce_kernel(const ReduceArgs p) {
+// One wave per token row.  lse2 = M + log2(sum_t s_t 2^(m_t - M)); then the
+// row of E becomes dZ = E * f_t - g [v == y], f_t = 2^(m_t - lse2) * g, in
+// fp32 and rounded to bf16 once (zero for an ignored row: g = 0).
+__global__ __launch_bounds__(256) void flce_row_kernel(const RowArgs p) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= p.nc) return;
-  float* m = p.mpart + row * p.nvt;
+  const float* m = p.mpart + row * p.nvt;
   const float* s = p.spart + row * p.nvt;
   float mx = -INFINITY;
   for (int64_t t = lane; t < p.nvt; t += 64) mx = fmaxf(mx, m[t]);
@@ -455,18 +410,29 @@ __global__ __launch_bounds__(256) void flce_reduce_kernel(const ReduceArgs p) {
   const int64_t yv = p.y[row];
   const bool valid = yv != p.ignore_index && yv >= 0 && yv < p.V;
   const float gv = valid ? *p.invden : 0.f;
-  for (int64_t t = lane; t < p.nvt; t += 64) m[t] = exp2f_fast(m[t] - lse2) * gv;
-  if (lane == 0) {
-    p.g[row] = gv;
-    p.loss_row[row] = valid ? lse2 * kLn2 - p.zy[row] : 0.f;
+  if (lane == 0) p.loss_row[row] = valid ? lse2 * kLn2 - p.zy[row] : 0.f;
+  // dZ, 8 columns per lane per step (V is a multiple of 8, so a chunk never
+  // straddles the row end; 8 aligned columns never straddle a 256-column tile)
+  bf16* e = p.E + row * p.V;
+  for (int64_t v0 = 8 * (int64_t)lane; v0 < p.V; v0 += 512) {
+    const float fv = exp2f_fast(m[v0 / kVT] - lse2) * gv;
+    const bf16x8 x = ld_bf16x8(e + v0);
+    bf16x8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (bf16)((float)x[i] * fv);
+    const int64_t yrel = yv - v0;
+    if (valid && yrel >= 0 && yrel < 8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = (i == yrel) ? (bf16)((float)x[i] * fv - gv) : o[i];
+    }
+    st_bf16x8(e + v0, o);
   }
 }
 
 // ---------------------------------------------------------------- dH
 struct DhArgs {
   GOp Wt;        // W [V, hdim] read as A[i = h][k = v]
-  GOp E;         // [nc, V] read as B[j = tok][k = v]
-  DzForm form;
+  GOp E;         // dZ [nc, V] read as B[j = tok][k = v]
   bf16* dh;      // dhidden rows of the chunk [nc, hdim] (used when splits == 1)
   float* part;   // [splits, nc, hdim]
   int64_t hdim, nc, kper;
@@ -482,7 +448,7 @@ __global__ __launch_bounds__(NT) void flce_dh_kernel(const DhArgs p) {
   const int64_t kb = split * p.kper;
   const int64_t ke = min(p.E.cols, kb + p.kper);
   f32x16 acc[4][2];
-  gemm_core<false, true, true>(smem, p.Wt, p.E, p.form, i0, j0, kb, ke, acc);
+  gemm_core<false, true>(smem, p.Wt, p.E, i0, j0, kb, ke, acc);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int wi = w & 1, wj = w >> 1;
 #pragma unroll
@@ -538,8 +504,7 @@ __global__ __launch_bounds__(256) void flce_dh_sum_kernel(const float* __restric
 // ---------------------------------------------------------------- dW
 struct DwArgs {
   GOp Ht;        // hidden rows of the chunk [nc, hdim] read as A[i = h][k = tok]
-  GOp Et;        // [nc, V] read as B[j = v][k = tok]
-  DzForm form;
+  GOp Et;        // dZ [nc, V] read as B[j = v][k = tok]
   bf16* dw;      // [V, hdim]
   float* acc32;  // [V, hdim] fp32 accumulator across chunks
   int64_t hdim, V;
@@ -553,7 +518,7 @@ __global__ __launch_bounds__(NT) void flce_dw_kernel(const DwArgs p) {
   if (!tile_of(p.nI, p.nJ, p.nI, ti, tj)) return;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
   f32x16 acc[4][2];
-  gemm_core<false, false, true>(smem, p.Ht, p.Et, p.form, i0, j0, 0, p.Ht.rows, acc);
+  gemm_core<false, false>(smem, p.Ht, p.Et, i0, j0, 0, p.Ht.rows, acc);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int wi = w & 1, wj = w >> 1;
 #pragma unroll
@@ -660,7 +625,7 @@ __global__ __launch_bounds__(256) void zero_bf16_kernel(bf16* __restrict__ x, in
 
 // ---------------------------------------------------------------- workspace
 struct Layout {
-  size_t invden, loss_row, g, mpart, spart, zy, E, part, acc32, total;
+  size_t invden, loss_row, mpart, spart, zy, E, part, acc32, total;
   int64_t chunk, nvt, splits;
 };
 
@@ -685,8 +650,6 @@ Layout layout(int64_t n, int64_t hdim, int64_t V, int64_t chunk, bool need_dw) {
   off += 256;
   L.loss_row = off;
   off += al(sizeof(float) * (size_t)(n > 0 ? n : 1));
-  L.g = off;
-  off += al(sizeof(float) * (size_t)L.chunk);
   L.mpart = off;
   off += al(sizeof(float) * (size_t)(L.chunk * L.nvt));
   L.spart = off;
@@ -715,7 +678,6 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
   char* ws = static_cast<char*>(a.ws);
   float* invden = reinterpret_cast<float*>(ws + L.invden);
   float* loss_row = reinterpret_cast<float*>(ws + L.loss_row);
-  float* g = reinterpret_cast<float*>(ws + L.g);
   float* mpart = reinterpret_cast<float*>(ws + L.mpart);
   float* spart = reinterpret_cast<float*>(ws + L.spart);
   float* zy = reinterpret_cast<float*>(ws + L.zy);
@@ -752,26 +714,23 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
       hipLaunchKernelGGL(flce_logits_kernel, dim3(grid), dim3(NT), 0, stream, lg);
     }
 
-    ReduceArgs rd{};
-    rd.mpart = mpart;
-    rd.spart = spart;
-    rd.zy = zy;
-    rd.y = yc;
-    rd.g = g;
-    rd.loss_row = loss_row + c0;
-    rd.invden = invden;
-    rd.nc = nc;
-    rd.nvt = L.nvt;
-    rd.V = V;
-    rd.ignore_index = a.ignore_index;
-    hipLaunchKernelGGL(flce_reduce_kernel, dim3((unsigned)((nc + 3) / 4)), dim3(256), 0, stream, rd);
-
-    DzForm form{mpart, g, yc, L.nvt, nc, V};
+    RowArgs rw{};
+    rw.mpart = mpart;
+    rw.spart = spart;
+    rw.zy = zy;
+    rw.y = yc;
+    rw.E = E;
+    rw.loss_row = loss_row + c0;
+    rw.invden = invden;
+    rw.nc = nc;
+    rw.nvt = L.nvt;
+    rw.V = V;
+    rw.ignore_index = a.ignore_index;
+    hipLaunchKernelGGL(flce_row_kernel, dim3((unsigned)((nc + 3) / 4)), dim3(256), 0, stream, rw);
 
     DhArgs dh{};
     dh.Wt = GOp{a.weight, Hd, V, Hd};
     dh.E = GOp{E, V, nc, V};
-    dh.form = form;
     dh.dh = a.dhidden + c0 * Hd;
     dh.part = part;
     dh.hdim = Hd;
@@ -800,7 +759,6 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
       DwArgs dw{};
       dw.Ht = GOp{Hc, Hd, nc, Hd};
       dw.Et = GOp{E, V, nc, V};
-      dw.form = form;
       dw.dw = a.dweight;
       dw.acc32 = acc32;
       dw.hdim = Hd;
