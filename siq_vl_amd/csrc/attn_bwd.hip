@@ -81,8 +81,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
   const bool kvvalid = kvrow < si.k_len;
   // K and V of the tile in LDS (rows past the end repeat the last row: they
   // only reach dK / dV rows that are never written)
-  kt.issue(p.k + (int64_t)(si.k_start + k0) * p.k_tok + (int64_t)hk * p.k_head, p.k_tok, si.k_len - k0, Ks, wu);
-  vt.issue(p.v + (int64_t)(si.k_start + k0) * p.v_tok + (int64_t)hk * p.v_head, p.v_tok, si.k_len - k0, Vs, wu);
+  kt.template issue<true>(p.k + (int64_t)(si.k_start + k0) * p.k_tok + (int64_t)hk * p.k_head, p.k_tok, si.k_len - k0,
+                          Ks, wu);
+  vt.template issue<true>(p.v + (int64_t)(si.k_start + k0) * p.v_tok + (int64_t)hk * p.v_head, p.v_tok, si.k_len - k0,
+                          Vs, wu);
   f32x16 dk[NDT], dv[NDT];
 #pragma unroll
   for (int i = 0; i < NDT; ++i) {
@@ -96,20 +98,30 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
   const int qb_last = (si.q_len - 1) / BM;
   const int s0 = it.s0, ns = it.s1 - it.s0;
 
+  // this wave's source tensor (Q or dO, and LSE2 or Delta), pinned so the
+  // step loop does not re-read the kernel arguments
+  const bf16* sbase = stages_q ? p.q : p.dout;
+  int64_t stok = stages_q ? p.q_tok : p.do_tok;
+  int64_t shead = stages_q ? p.q_head : p.do_head;
+  const float* rbase = stages_q ? p.lse2 : p.delta;
+  int64_t lhead = p.lse_head;
+  pin_sgpr(sbase);
+  pin_sgpr(stok);
+  pin_sgpr(shead);
+  pin_sgpr(rbase);
+  pin_sgpr(lhead);
+  // loads untracked: the step loop's wait_vmem + barrier order them
   auto issue = [&](int step, int buf) {
     const int j = step % p.n_rep, qb = qb_last - step / p.n_rep;
     const int hq = hk * p.n_rep + j;
     const int q0 = qb * BM;
     const int nrows = si.q_len - q0;
     const int64_t r0 = si.q_start + q0;
-    const bf16* src = stages_q ? p.q + r0 * p.q_tok + (int64_t)hq * p.q_head
-                               : p.dout + r0 * p.do_tok + (int64_t)hq * p.do_head;
-    st.issue(src, stages_q ? p.q_tok : p.do_tok, nrows, smem + buf * STAGE + (stages_q ? 0 : TE), wu & 3);
+    st.template issue<true>(sbase + r0 * stok + (int64_t)hq * shead, stok, nrows,
+                            smem + buf * STAGE + (stages_q ? 0 : TE), wu & 3);
     if (stages_row) {
       const uint32_t r = (uint32_t)min(lane, nrows - 1);
-      const float* rs = (stages_q ? p.lse2 : p.delta) + (int64_t)hq * p.lse_head + r0;
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(rs) + (r << 2),
-                                       (lds_void*)(&rowv[buf][stages_q ? 0 : 1][0]), 4, 0, 0);
+      dma4_untracked(rbase + (int64_t)hq * lhead + r0 + r, &rowv[buf][stages_q ? 0 : 1][0]);
     }
   };
 
@@ -369,9 +381,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
 
   const bf16* kbase = p.k + (int64_t)si.k_start * p.k_tok + (int64_t)hk * p.k_head;
   const bf16* vbase = p.v + (int64_t)si.k_start * p.v_tok + (int64_t)hk * p.v_head;
+  // loads untracked: the block loop's wait_vmem + barrier order them
   auto issue = [&](int kb, int buf) {
-    kt.issue(kbase + (int64_t)(kb * BN) * p.k_tok, p.k_tok, si.k_len - kb * BN, smem + buf * STAGE, g);
-    vt.issue(vbase + (int64_t)(kb * BN) * p.v_tok, p.v_tok, si.k_len - kb * BN, smem + buf * STAGE + TE, g);
+    kt.template issue<true>(kbase + (int64_t)(kb * BN) * p.k_tok, p.k_tok, si.k_len - kb * BN, smem + buf * STAGE, g);
+    vt.template issue<true>(vbase + (int64_t)(kb * BN) * p.v_tok, p.v_tok, si.k_len - kb * BN,
+                            smem + buf * STAGE + TE, g);
   };
   if (nblk > 0) issue(0, 0);
   wait_vmem();

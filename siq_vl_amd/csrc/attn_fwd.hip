@@ -84,9 +84,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
 
   const bf16* kbase = p.k + (int64_t)si.k_start * p.k_tok + (int64_t)hk * p.k_head;
   const bf16* vbase = p.v + (int64_t)si.k_start * p.v_tok + (int64_t)hk * p.v_head;
+  // K / V loads are untracked: each block's wait_vmem + barrier orders them
   if (nblk > 0) {
-    kt.issue(kbase, p.k_tok, si.k_len, smem, wu);
-    vt.issue(vbase, p.v_tok, si.k_len, smem + TE, wu);
+    kt.template issue<true>(kbase, p.k_tok, si.k_len, smem, wu);
+    vt.template issue<true>(vbase, p.v_tok, si.k_len, smem + TE, wu);
   }
   wait_vmem();
   __syncthreads();
@@ -99,8 +100,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
     const bool more = kb + 1 < nblk;
     if (more) {
       bf16* nx = smem + ((kb + 1) & 1) * STAGE;
-      kt.issue(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN, nx, wu);
-      vt.issue(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN, nx + TE, wu);
+      kt.template issue<true>(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN, nx, wu);
+      vt.template issue<true>(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN, nx + TE, wu);
     }
     const bool active = !CAUSAL || (k0 <= wq_last + off);
     if (active) {

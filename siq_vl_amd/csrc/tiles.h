@@ -150,6 +150,22 @@ struct TrRead {
   }
 };
 
+// One dword per lane from gptr straight into LDS (lane l's 4 bytes land at LDS
+// byte lds + 4 l), untracked like LdsTile::issue<true>: the caller orders it
+// with wait_vmem and a barrier.  s_nop 0: m0 needs one wait state after its
+// write; the address is a VGPR pair.
+__device__ __forceinline__ void dma4_untracked(const void* gptr, const void* lds) {
+  const uint32_t la = (uint32_t)(uintptr_t)(lds_void*)lds;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(gptr), "{m0}"(la) : "memory");
+}
+
+// Makes a wave-uniform value opaque, so the compiler keeps it in SGPRs rather
+// than re-reading it from the kernel arguments on every trip of a loop.
+template <typename T>
+__device__ __forceinline__ void pin_sgpr(T& x) {
+  asm volatile("" : "+s"(x));
+}
+
 // Wait for this wave's outstanding global (and direct-to-LDS) loads.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
