@@ -270,42 +270,49 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
 
 // dK / dV of split tiles: the pieces' fp32 sums added in piece order (so the
 // result does not depend on which piece ran when), scaled and written as bf16.
-// One workgroup = one split tile and kv-head; thread x owns float4 column
-// x % (2 D / 4) of [dK | dV] and rows x / (2 D / 4) + RSTEP i, 8 rows at a
-// time so that their loads are in flight together.
+// One workgroup = ROWS rows of one split tile and kv-head (blockIdx.x = tile *
+// NCH + row chunk); thread x owns float4 column x % COLS of [dK | dV] and
+// rows x / COLS + RSTEP u (u < U) of the chunk, whose loads are in flight
+// together.
+template <int D>
+struct DkvSum {
+  static constexpr int C4 = D / 4, COLS = 2 * C4, RSTEP = 256 / COLS, U = 8, ROWS = RSTEP * U, NCH = kBwdBN / ROWS;
+  static_assert(kBwdBN % ROWS == 0, "rows split evenly");
+};
+
 template <int D>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_sum_kernel(const AttnParams p) {
-  constexpr int BN = kBwdBN, C4 = D / 4, COLS = 2 * C4, RSTEP = 256 / COLS, U = 8;
-  static_assert(BN % (RSTEP * U) == 0, "rows split evenly");
-  if ((int)blockIdx.x >= *p.nsplit) return;
-  const SplitTile st = p.splits[blockIdx.x];
+  using S = DkvSum<D>;
+  constexpr int BN = kBwdBN;
+  const int tile = blockIdx.x / S::NCH, ch = blockIdx.x % S::NCH;
+  if (tile >= *p.nsplit) return;
+  const SplitTile st = p.splits[tile];
   const SeqInfo si = p.seq[st.b];
   const int hk = blockIdx.y;
   if ((st.slot0 + st.np) * p.hkv > kSplitSlots) return;
-  const int col = threadIdx.x % COLS, which = col / C4, c = col - which * C4;
+  const int col = threadIdx.x % S::COLS, which = col / S::C4, c = col - which * S::C4;
   const int k0 = st.t * BN;
   const int rows = min(BN, si.k_len - k0);
+  const int r0 = ch * S::ROWS + threadIdx.x / S::COLS;
   const float* base = p.dkv_part + (int64_t)(st.slot0 * p.hkv + hk) * (2 * BN * D) + (int64_t)which * BN * D + 4 * c;
   const int64_t pstride = (int64_t)p.hkv * (2 * BN * D);
   const float sc = which == 0 ? p.scale : 1.f;
-  for (int r0 = threadIdx.x / COLS; r0 < BN; r0 += RSTEP * U) {
-    f32x4 acc[U];
+  f32x4 acc[S::U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc[u] = *reinterpret_cast<const f32x4*>(base + (int64_t)(r0 + RSTEP * u) * D);
-    for (int pc = 1; pc < st.np; ++pc)
+  for (int u = 0; u < S::U; ++u) acc[u] = *reinterpret_cast<const f32x4*>(base + (int64_t)(r0 + S::RSTEP * u) * D);
+  for (int pc = 1; pc < st.np; ++pc)
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        acc[u] += *reinterpret_cast<const f32x4*>(base + pc * pstride + (int64_t)(r0 + RSTEP * u) * D);
+    for (int u = 0; u < S::U; ++u)
+      acc[u] += *reinterpret_cast<const f32x4*>(base + pc * pstride + (int64_t)(r0 + S::RSTEP * u) * D);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int r = r0 + RSTEP * u;
-      if (r >= rows) continue;
-      const int64_t row = si.k_start + k0 + r;
-      bf16* dst = which == 0 ? p.dk + row * p.dk_tok + (int64_t)hk * p.dk_head + 4 * c
-                             : p.dv + row * p.dv_tok + (int64_t)hk * p.dv_head + 4 * c;
-      *reinterpret_cast<bf16x4*>(dst) = bf16x4{(bf16)(acc[u][0] * sc), (bf16)(acc[u][1] * sc), (bf16)(acc[u][2] * sc),
-                                               (bf16)(acc[u][3] * sc)};
-    }
+  for (int u = 0; u < S::U; ++u) {
+    const int r = r0 + S::RSTEP * u;
+    if (r >= rows) continue;
+    const int64_t row = si.k_start + k0 + r;
+    bf16* dst = which == 0 ? p.dk + row * p.dk_tok + (int64_t)hk * p.dk_head + 4 * c
+                           : p.dv + row * p.dv_tok + (int64_t)hk * p.dv_head + 4 * c;
+    *reinterpret_cast<bf16x4*>(dst) = bf16x4{(bf16)(acc[u][0] * sc), (bf16)(acc[u][1] * sc), (bf16)(acc[u][2] * sc),
+                                             (bf16)(acc[u][3] * sc)};
   }
 }
 
@@ -468,7 +475,8 @@ hipError_t launch_bwd_t(const AttnParams& p, int qcap, int kvcap, hipStream_t st
   hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)qcap * p.hq)), dim3(256), 0, stream, p);
   hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)kvcap * p.hkv)), dim3(512), 0, stream,
                      p);
-  hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D>), dim3(kMaxSplitTiles, p.hkv), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D>), dim3(kMaxSplitTiles * DkvSum<D>::NCH, p.hkv), dim3(256), 0, stream,
+                     p);
   return hipGetLastError();
 }
 
