@@ -128,6 +128,19 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
   if (ns > 0) issue(s0, 0);
   wait_vmem();
   __syncthreads();
+  // At D = 64 this wave's 32 kv rows of K and V stay in registers as the B
+  // operands of S = Q K^T and dP = dO V^T for every step of the item (a third
+  // of the step's LDS reads); at D = 128 they do not fit beside the dK / dV
+  // accumulators and are read from LDS each step.
+  constexpr bool KVREG = D <= 64;
+  bf16x8 kreg[KVREG ? D / 16 : 1], vreg[KVREG ? D / 16 : 1];
+  if constexpr (KVREG) {
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      kreg[ks] = rr.read(Ks, 32 * kq, ks);
+      vreg[ks] = rr.read(Vs, 32 * kq, ks);
+    }
+  }
 
   for (int i = 0; i < ns; ++i) {
     const int step = s0 + i;
@@ -148,20 +161,29 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
       f32x16 s = zero16(), dp = zero16();
       bf16x8 fq[2], fg[2], fk[2], fv[2];
       fq[0] = rr.read(Qs, 32 * g, 0);
-      fk[0] = rr.read(Ks, 32 * kq, 0);
       fg[0] = rr.read(Gs, 32 * g, 0);
-      fv[0] = rr.read(Vs, 32 * kq, 0);
+      if constexpr (!KVREG) {
+        fk[0] = rr.read(Ks, 32 * kq, 0);
+        fv[0] = rr.read(Vs, 32 * kq, 0);
+      }
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
         const int cur = ks & 1;
         if (ks + 1 < D / 16) {
           fq[cur ^ 1] = rr.read(Qs, 32 * g, ks + 1);
-          fk[cur ^ 1] = rr.read(Ks, 32 * kq, ks + 1);
           fg[cur ^ 1] = rr.read(Gs, 32 * g, ks + 1);
-          fv[cur ^ 1] = rr.read(Vs, 32 * kq, ks + 1);
+          if constexpr (!KVREG) {
+            fk[cur ^ 1] = rr.read(Ks, 32 * kq, ks + 1);
+            fv[cur ^ 1] = rr.read(Vs, 32 * kq, ks + 1);
+          }
         }
-        s = mfma32(fq[cur], fk[cur], s);
-        dp = mfma32(fg[cur], fv[cur], dp);
+        if constexpr (KVREG) {
+          s = mfma32(fq[cur], kreg[ks], s);
+          dp = mfma32(fg[cur], vreg[ks], dp);
+        } else {
+          s = mfma32(fq[cur], fk[cur], s);
+          dp = mfma32(fg[cur], fv[cur], dp);
+        }
       }
       // P = exp2(S scale log2e - LSE2), dS = P (dP - Delta), in place; on the
       // causal diagonal and past the end of the sequence the exponent is -inf
