@@ -23,11 +23,20 @@ constexpr int kSplitSlots = 2 * kSplitTarget + 2;  // bound on sum(pieces x hkv)
 constexpr int kMaxSplitTiles = kSplitSlots / 2;    // a split tile has >= 2 pieces
 constexpr int kXcds = 8;                           // MI355X: workgroup b runs on XCD b % 8
 
-// One dK/dV work item: steps [s0, s1) of kv tile t of sequence b; piece `piece`
-// of np (np == 1: the whole tile, written directly as bf16).  Steps walk the
-// q blocks downwards from the last one, each over the n_rep q-heads.  A piece
-// of a split tile writes fp32 sums to slot (slot0 + piece) * hkv + hk.
+// One forward / dQ work unit: q tile t of sequence b (b < 0: idle), with the
+// sequence's extents copied in, so a workgroup starts from one load of its
+// entry rather than two dependent ones.
+struct QTile {
+  SeqInfo s;
+  int b, t, pad0, pad1;
+};
+// One dK/dV work item: steps [s0, s1) of kv tile t of sequence b (extents in
+// s; b < 0: idle); piece `piece` of np (np == 1: the whole tile, written
+// directly as bf16).  Steps walk the q blocks downwards from the last one,
+// each over the n_rep q-heads.  A piece of a split tile writes fp32 sums to
+// slot (slot0 + piece) * hkv + hk.
 struct KvItem {
+  SeqInfo s;
   int b, t, s0, s1, piece, np, slot0, pad;
 };
 // A split tile, for the kernel that adds its pieces' partial sums.
@@ -61,7 +70,7 @@ struct AttnParams {
   float* delta;      // [hq, lse_head] rowsum(dO * O) (backward workspace)
   float* lse2;       // [hq, lse_head] LSE * log2(e) (backward workspace)
   const SeqInfo* seq;
-  const int2* qtiles;   // (sequence, q-tile) ordered by decreasing work; x < 0 = idle
+  const QTile* qtiles;       // q tiles ordered by decreasing work; b < 0 = idle
   const KvItem* kvitems;     // dK/dV work items (longest sequences first); b < 0 = idle
   float* dkv_part;           // [kSplitSlots][2][kBwdBN][D] fp32 partial dK / dV of split tiles
   const SplitTile* splits;   // [kMaxSplitTiles] split tiles
@@ -82,7 +91,7 @@ inline int64_t tile_cap(int64_t total, int batch, int rows) { return total / row
 inline int64_t kv_item_cap(int64_t total_k, int batch) { return tile_cap(total_k, batch, kBwdBN) + kSplitTarget + 1; }
 
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,
-                           int causal, int n_rep, int hkv, SeqInfo* seq, int2* qtiles, int qrows, int qcap,
+                           int causal, int n_rep, int hkv, SeqInfo* seq, QTile* qtiles, int qrows, int qcap,
                            KvItem* kvitems, int kvcap, int* seqbuf, SplitTile* splits, int* nsplit,
                            hipStream_t stream);
 hipError_t launch_attn_fwd(const AttnParams& p, int d, int causal, int qcap, hipStream_t stream);

@@ -71,8 +71,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
   const int e = xcd_order(blockIdx.x, gridDim.x, 32);
   const int ii = e / p.hkv, hk = e - ii * p.hkv;
   const KvItem it = p.kvitems[ii];
+  // every field loaded before the idle test (the compiler would otherwise
+  // fetch b alone, wait for it, then fetch the rest)
+  asm volatile("" : : "s"(it.s.q_start), "s"(it.s.q_len), "s"(it.s.k_start), "s"(it.s.k_len), "s"(it.t), "s"(it.s0),
+               "s"(it.s1));
   if (it.b < 0) return;
-  const SeqInfo si = p.seq[it.b];
+  const SeqInfo si = it.s;
   const int k0 = it.t * BN;
   const int kb = k0 + 32 * kq;  // first kv row of this wave
   const int off = si.k_len - si.q_len;
@@ -363,10 +367,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
   // entries (its resident workgroups), whole tiles at a time
   const int e = xcd_order(blockIdx.x, gridDim.x, p.hq * max(1, 64 / p.hq));
   const int ti = e / p.hq, hqi = e - ti * p.hq, hk = hqi / p.n_rep;
-  const int2 tl = p.qtiles[ti];
-  if (tl.x < 0) return;
-  const SeqInfo si = p.seq[tl.x];
-  const int q0 = tl.y * BM;
+  const QTile tl = p.qtiles[ti];
+  // every field loaded before the idle test (the compiler would otherwise
+  // fetch b alone, wait for it, then fetch the rest)
+  asm volatile("" : : "s"(tl.s.q_start), "s"(tl.s.q_len), "s"(tl.s.k_start), "s"(tl.s.k_len), "s"(tl.t));
+  if (tl.b < 0) return;
+  const SeqInfo si = tl.s;
+  const int q0 = tl.t * BM;
   const int off = si.k_len - si.q_len;
   int kv_end = si.k_len;
   if (CAUSAL) kv_end = min(kv_end, q0 + BM + off);

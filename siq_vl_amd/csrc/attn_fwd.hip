@@ -55,10 +55,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   // entries (its resident workgroups), whole tiles at a time
   const int e = xcd_order(blockIdx.x, gridDim.x, p.hq * max(1, 64 / p.hq));
   const int ti = e / p.hq, hqi = e - ti * p.hq, hk = hqi / p.n_rep;
-  const int2 tl = p.qtiles[ti];
-  if (tl.x < 0) return;
-  const SeqInfo si = p.seq[tl.x];
-  const int q0 = tl.y * BM;
+  const QTile tl = p.qtiles[ti];
+  // every field loaded before the idle test (the compiler would otherwise
+  // fetch b alone, wait for it, then fetch the rest)
+  asm volatile("" : : "s"(tl.s.q_start), "s"(tl.s.q_len), "s"(tl.s.k_start), "s"(tl.s.k_len), "s"(tl.t));
+  if (tl.b < 0) return;
+  const SeqInfo si = tl.s;
+  const int q0 = tl.t * BM;
   const int off = si.k_len - si.q_len;
   int kv_end = si.k_len;
   if (CAUSAL) kv_end = min(kv_end, q0 + BM + off);

@@ -48,7 +48,7 @@ AttnLayout attn_layout(int batch, int64_t total_q, int64_t total_k, int hq, int 
   L.seq = off;
   off += align256(sizeof(siq::SeqInfo) * (size_t)(batch > 0 ? batch : 1));
   L.qtiles = off;
-  off += align256(sizeof(int2) * (size_t)L.qcap);
+  off += align256(sizeof(siq::QTile) * (size_t)L.qcap);
   L.kvitems = off;
   off += align256(sizeof(siq::KvItem) * (size_t)L.kvcap);
   L.seqbuf = off;
@@ -140,7 +140,7 @@ int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, fl
   p.out = static_cast<siq::bf16*>(o);
   p.lse = lse;
   p.seq = reinterpret_cast<const siq::SeqInfo*>(base + L.seq);
-  p.qtiles = reinterpret_cast<const int2*>(base + L.qtiles);
+  p.qtiles = reinterpret_cast<const siq::QTile*>(base + L.qtiles);
   p.batch = batch;
   p.hq = hq;
   p.hkv = hkv;
@@ -161,7 +161,7 @@ int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, fl
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0, hq / hkv, hkv,
                                       reinterpret_cast<siq::SeqInfo*>(base + L.seq),
-                                      reinterpret_cast<int2*>(base + L.qtiles), siq::kFwdBM, L.qcap, nullptr, 0,
+                                      reinterpret_cast<siq::QTile*>(base + L.qtiles), siq::kFwdBM, L.qcap, nullptr, 0,
                                       nullptr, nullptr, nullptr, s);
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
   e = siq::launch_attn_fwd(p, d, causal != 0, L.qcap, s);
@@ -204,7 +204,7 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
   p.delta = reinterpret_cast<float*>(base + L.delta);
   p.lse2 = reinterpret_cast<float*>(base + L.lse2);
   p.seq = reinterpret_cast<const siq::SeqInfo*>(base + L.seq);
-  p.qtiles = reinterpret_cast<const int2*>(base + L.qtiles);
+  p.qtiles = reinterpret_cast<const siq::QTile*>(base + L.qtiles);
   p.kvitems = reinterpret_cast<const siq::KvItem*>(base + L.kvitems);
   p.dkv_part = reinterpret_cast<float*>(base + L.part);
   p.splits = reinterpret_cast<const siq::SplitTile*>(base + L.splits);
@@ -237,7 +237,7 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0, hq / hkv, hkv,
                                       reinterpret_cast<siq::SeqInfo*>(base + L.seq),
-                                      reinterpret_cast<int2*>(base + L.qtiles), siq::kFwdBM, L.qcap,
+                                      reinterpret_cast<siq::QTile*>(base + L.qtiles), siq::kFwdBM, L.qcap,
                                       reinterpret_cast<siq::KvItem*>(base + L.kvitems), L.kvcap,
                                       reinterpret_cast<int*>(base + L.seqbuf),
                                       reinterpret_cast<siq::SplitTile*>(base + L.splits),

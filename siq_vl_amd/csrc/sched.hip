@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
                                                                  const int* __restrict__ cu_k, int batch,
                                                                  int64_t total_q, int64_t total_k, int causal,
                                                                  int n_rep, int hkv, SeqInfo* __restrict__ seq,
-                                                                 int2* __restrict__ qtiles, int qrows, int qcap,
+                                                                 QTile* __restrict__ qtiles, int qrows, int qcap,
                                                                  KvItem* __restrict__ kvitems, int kvcap,
                                                                  int* __restrict__ seqbuf,
                                                                  SplitTile* __restrict__ splits,
@@ -144,10 +144,10 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
       const int nt = (s.q_len + qrows - 1) / qrows;
       for (int t = 0; t < nt; ++t) {
         const int pos = atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(s, t, qrows, causal)], 1);
-        if (pos < qcap) qtiles[pos] = make_int2(b, t);
+        if (pos < qcap) qtiles[pos] = QTile{s, b, t, 0, 0};
       }
     }
-    for (int i = total + tid; i < qcap; i += kSchedThreads) qtiles[i] = make_int2(-1, -1);
+    for (int i = total + tid; i < qcap; i += kSchedThreads) qtiles[i] = QTile{SeqInfo{0, 0, 0, 0}, -1, -1, 0, 0};
     return;
   }
 
@@ -217,6 +217,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
     for (int pc = 0; pc < np; ++pc) {
       const int pos = atomicAdd(&hist[kSchedKeys - 1 - clamp_key(min(S, w - pc * S))], 1);
       KvItem it;
+      it.s = s;
       it.b = b;
       it.t = t;
       it.s0 = pc * S;
@@ -240,7 +241,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
 }  // namespace
 
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,
-                           int causal, int n_rep, int hkv, SeqInfo* seq, int2* qtiles, int qrows, int qcap,
+                           int causal, int n_rep, int hkv, SeqInfo* seq, QTile* qtiles, int qrows, int qcap,
                            KvItem* kvitems, int kvcap, int* seqbuf, SplitTile* splits, int* nsplit,
                            hipStream_t stream) {
   const int blocks = kvitems != nullptr ? 2 : 1;
