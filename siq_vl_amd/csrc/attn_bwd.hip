@@ -39,9 +39,9 @@ template <int D, bool CAUSAL>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams p) {
   constexpr int BN = kBwdBN, BM = kBwdBM, NT = 512, NW = NT / 64, NS = 2;
   static_assert(BN == 128 && BM == 64, "128 kv rows (4 x 32) by 64 q rows (2 x 32) per step");
-  using QTile = LdsTile<BM, D, NW / 2>;  // Q staged by waves 0-3, dO by waves 4-7
+  using StTile = LdsTile<BM, D, NW / 2>;  // Q staged by waves 0-3, dO by waves 4-7
   using KVTile = LdsTile<BN, D, NW>;
-  constexpr int TE = QTile::ELEMS;
+  constexpr int TE = StTile::ELEMS;
   constexpr int STAGE = 2 * TE;  // Q, dO (bf16 elements)
   constexpr int NDT = D / 32;
   constexpr int SMEM = NS * STAGE + 2 * KVTile::ELEMS;  // stages, K, V
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
   const int g = wu & 1, kq = wu >> 1;     // q group (32 rows of a step), kv quarter (32 rows of the tile)
   const bool stages_q = wu < 4;           // waves 0-3 stage Q, waves 4-7 stage dO
   const bool stages_row = (wu & 3) == 0;  // waves 0 / 4 also stage the step's LSE2 / Delta
-  QTile st;
+  StTile st;
   st.init(stages_q ? p.q_tok : p.do_tok, lane);
   KVTile kt, vt;
   kt.init(p.k_tok, lane);
@@ -114,20 +114,34 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
   pin_sgpr(shead);
   pin_sgpr(rbase);
   pin_sgpr(lhead);
-  // loads untracked: the step loop's wait_vmem + barrier order them
-  auto issue = [&](int step, int buf) {
+  // Loads untracked: the step loop's wait_vmem + barrier order them.  A step's
+  // loads are described once (src, nrows, buf) and issued one instruction at
+  // a time (issue_k), spread over the previous step's S / dP MFMAs so that the
+  // waves do not all wait on the load queue at the start of a step.
+  struct StepLoad {
+    const bf16* src;
+    const float* rsrc;
+    int nrows, buf;
+  };
+  auto describe = [&](int step, int buf) {
     const int j = step % p.n_rep, qb = qb_last - step / p.n_rep;
     const int hq = hk * p.n_rep + j;
     const int q0 = qb * BM;
-    const int nrows = si.q_len - q0;
     const int64_t r0 = si.q_start + q0;
-    st.template issue<true>(sbase + r0 * stok + (int64_t)hq * shead, stok, nrows,
-                            smem + buf * STAGE + (stages_q ? 0 : TE), wu & 3);
-    if (stages_row) {
-      const uint32_t r = (uint32_t)min(lane, nrows - 1);
-      dma4_untracked(rbase + (int64_t)hq * lhead + r0 + r, &rowv[buf][stages_q ? 0 : 1][0]);
-    }
+    return StepLoad{sbase + r0 * stok + (int64_t)hq * shead, rbase + (int64_t)hq * lhead + r0, si.q_len - q0, buf};
   };
+  auto issue_k = [&](const StepLoad& l, int k) {
+    st.template issue_one<true>(k, l.src, stok, l.nrows, smem + l.buf * STAGE + (stages_q ? 0 : TE), wu & 3);
+    if (k == 0 && stages_row)
+      dma4_untracked(l.rsrc + min(lane, l.nrows - 1), &rowv[l.buf][stages_q ? 0 : 1][0]);
+  };
+  auto issue = [&](int step, int buf) {
+    const StepLoad l = describe(step, buf);
+#pragma unroll
+    for (int k = 0; k < StTile::PERW; ++k) issue_k(l, k);
+  };
+  constexpr int KPI = (D / 16) / StTile::PERW;  // S / dP k-steps per spread load instruction
+  static_assert(KPI >= 1 && (D / 16) % StTile::PERW == 0, "loads spread evenly over the k-steps");
 
   if (ns > 0) issue(s0, 0);
   wait_vmem();
@@ -155,10 +169,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
     const float* dlt = rowv[buf][1];
     const int q0 = (qb_last - step / p.n_rep) * BM;
     const int qvalid = si.q_len - q0;  // rows of this block that exist
-    if (i + 1 < ns) issue(step + 1, buf ^ 1);
+    const bool pf = i + 1 < ns;
+    const StepLoad nl = describe(step + 1, buf ^ 1);
 
     const int wq0 = q0 + 32 * g;  // first q row of this wave
     const bool active = 32 * g < qvalid && (!CAUSAL || wq0 + 31 + off >= kb);
+    if (!active && pf) {
+#pragma unroll
+      for (int k = 0; k < StTile::PERW; ++k) issue_k(nl, k);
+    }
     if (active) {
       // accumulator r (= 8j + i) holds q = wq0 + 16j + 8(i / 4) + 4h + i % 4, kv = kvrow
       // operand fragments double-buffered one k-step ahead of the MFMAs
@@ -173,6 +192,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
         const int cur = ks & 1;
+        if (pf && ks % KPI == 0) issue_k(nl, ks / KPI);
         if (ks + 1 < D / 16) {
           fq[cur ^ 1] = rr.read(Qs, 32 * g, ks + 1);
           fg[cur ^ 1] = rr.read(Gs, 32 * g, ks + 1);

@@ -73,25 +73,31 @@ struct LdsTile {
   // read.  The caller then orders them itself (wait_vmcnt, then a barrier).
   template <bool UNTRACKED = false>
   __device__ __forceinline__ void issue(const bf16* gbase, int64_t stride, int nrows, bf16* lds, int wu) const {
-    const uint32_t st = (uint32_t)stride;
 #pragma unroll
-    for (int k = 0; k < PERW; ++k) {
-      const int i = wu * PERW + k;
-      int r = i * RPI + lrow;
-      if (nrows < ROWS) r = min(r, nrows - 1);
-      const uint32_t o = (uint32_t)r * st + coff[k % PAT];
-      if constexpr (UNTRACKED) {
-        // lane l's 16 bytes land at LDS byte m0 + 16 l.  s_nop 4: m0 needs one wait state after its
-        // write, and the base SGPRs may have been written by a VALU instruction (an SGPR written by
-        // VALU and read by VMEM needs five), which the compiler's hazard checks do not see in asm.
-        const uint32_t la = (uint32_t)(uintptr_t)(lds_void*)(lds + i * 512);
-        asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(o << 1), "s"(gbase), "{m0}"(la)
-                     : "memory");
-      } else {
-        // uniform base + 32-bit byte offset: the saddr + voffset form
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(gbase) + (o << 1), (lds_void*)(lds + i * 512),
-                                         16, 0, 0);
-      }
+    for (int k = 0; k < PERW; ++k) issue_one<UNTRACKED>(k, gbase, stride, nrows, lds, wu);
+  }
+
+  // Instruction k (< PERW) of this wave's share, so that a caller can spread
+  // its loads between other work.
+  template <bool UNTRACKED = false>
+  __device__ __forceinline__ void issue_one(int k, const bf16* gbase, int64_t stride, int nrows, bf16* lds,
+                                            int wu) const {
+    const uint32_t st = (uint32_t)stride;
+    const int i = wu * PERW + k;
+    int r = i * RPI + lrow;
+    if (nrows < ROWS) r = min(r, nrows - 1);
+    const uint32_t o = (uint32_t)r * st + coff[k % PAT];
+    if constexpr (UNTRACKED) {
+      // lane l's 16 bytes land at LDS byte m0 + 16 l.  s_nop 4: m0 needs one wait state after its
+      // write, and the base SGPRs may have been written by a VALU instruction (an SGPR written by
+      // VALU and read by VMEM needs five), which the compiler's hazard checks do not see in asm.
+      const uint32_t la = (uint32_t)(uintptr_t)(lds_void*)(lds + i * 512);
+      asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(o << 1), "s"(gbase), "{m0}"(la)
+                   : "memory");
+    } else {
+      // uniform base + 32-bit byte offset: the saddr + voffset form
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(gbase) + (o << 1), (lds_void*)(lds + i * 512),
+                                       16, 0, 0);
     }
   }
 };
