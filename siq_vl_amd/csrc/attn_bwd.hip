@@ -447,16 +447,34 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
   wait_vmem();
   __syncthreads();
 
+  // The next block's K (instructions 0 .. PERW - 1 of this wave) and V (PERW
+  // .. 2 PERW - 1) go out one at a time between this block's S / dP MFMAs: K
+  // during the first kv half, V during the second.
+  constexpr int KPI = (D / 16) / Tile::PERW;
+  static_assert(KPI >= 1 && (D / 16) % Tile::PERW == 0, "loads spread evenly over the k-steps");
   const int wq0 = q0 + 32 * g;
   for (int kb = 0; kb < nblk; ++kb) {
     const bf16* Ks = smem + (kb & 1) * STAGE;
     const bf16* Vs = Ks + TE;
-    if (kb + 1 < nblk) issue(kb + 1, (kb + 1) & 1);
+    const bool pf = kb + 1 < nblk;
+    const int nb = (kb + 1) * BN;  // first kv row of the next block
+    bf16* nx = smem + ((kb + 1) & 1) * STAGE;
+    auto issue_k = [&](int idx) {
+      if (idx < Tile::PERW)
+        kt.template issue_one<true>(idx, kbase + (int64_t)nb * p.k_tok, p.k_tok, si.k_len - nb, nx, g);
+      else
+        vt.template issue_one<true>(idx - Tile::PERW, vbase + (int64_t)nb * p.v_tok, p.v_tok, si.k_len - nb, nx + TE,
+                                    g);
+    };
     // the step's two 32-row kv halves in turn
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
     const int kw = kb * BN + 32 * kh;  // first kv row of this half
     const bool active = kw < si.k_len && (!CAUSAL || kw <= wq0 + 31 + off);
+    if (!active && pf) {
+#pragma unroll
+      for (int k = 0; k < Tile::PERW; ++k) issue_k(kh * Tile::PERW + k);
+    }
     if (active) {
       // accumulator r holds kv = kw + nrow(r, h) for q = qrow (operands one k-step ahead)
       f32x16 s = zero16(), dp = zero16();
@@ -466,6 +484,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
         const int cur = ks & 1;
+        if (pf && ks % KPI == 0) issue_k(kh * Tile::PERW + ks / KPI);
         if (ks + 1 < D / 16) {
           fk[cur ^ 1] = rr.read(Ks, 32 * kh, ks + 1);
           fv[cur ^ 1] = rr.read(Vs, 32 * kh, ks + 1);
