@@ -31,6 +31,7 @@ import torch
 
 from siq_vl_amd import attention as A
 from siq_vl_amd import cross_entropy as C
+from siq_vl_amd import rope as R
 from siq_vl_amd import workloads as W
 
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CUs x 2.4 GHz)
@@ -108,6 +109,68 @@ def bench_attention(steps: int, warmup: int) -> dict:
         "bytes_bwd": bytes_bwd,
         "pairs": pairs,
     }
+
+
+def _rope_inputs(cfg, dev):
+    """Config-2 q / k as Qwen2Attention hands them to apply_rotary_pos_emb ([1, H, T, D]
+    views of the [1, T, H*D] projections), position ids restarting per sequence."""
+    g = torch.Generator().manual_seed(W.SEED)
+    t, d = cfg.total, cfg.d
+    proj = lambda h: torch.randn(1, t, h * d, generator=g).to(torch.bfloat16).to(dev).view(1, t, h, d).transpose(1, 2)
+    q, k = proj(cfg.hq), proj(cfg.hkv)
+    cu = cfg.cu_seqlens().tolist()
+    pos = torch.cat([torch.arange(cu[i + 1] - cu[i]) for i in range(len(cu) - 1)]).float()
+    inv = 1.0 / (1000000.0 ** (torch.arange(0, d, 2).float() / d))
+    emb = torch.cat([pos[:, None] * inv, pos[:, None] * inv], dim=-1)[None]
+    cos, sin = emb.cos().to(torch.bfloat16).to(dev), emb.sin().to(torch.bfloat16).to(dev)
+    dq = torch.randn(q.shape, generator=g).to(torch.bfloat16).to(dev)
+    dk = torch.randn(k.shape, generator=g).to(torch.bfloat16).to(dev)
+    return q, k, cos, sin, dq, dk
+
+
+def bench_rope(steps: int, warmup: int) -> dict:
+    """Fused RoPE forward and backward at the config-2 shape; the reference's own
+    torch ops (modeling_qwen2.py:105-135 and their autograd) timed beside it."""
+    cfg = W.attn_config(2)
+    dev = torch.device("cuda")
+    q, k, cos, sin, gq, gk = _rope_inputs(cfg, dev)
+    bq, bk = R._bshd(q, 1), R._bshd(k, 1)
+    bgq, bgk = R._bshd(gq, 1), R._bshd(gk, 1)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ev = _events(steps + 1)
+        ev[0].record(stream)
+        for i in range(steps):
+            fn()
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+        return per[len(per) // 2]
+
+    fwd_ms = timed(lambda: R.rope_fwd(bq, bk, cos, sin))
+    bwd_ms = timed(lambda: R.rope_bwd(bgq, bgk, cos, sin))
+
+    def rh(x):
+        return torch.cat((-x[..., x.shape[-1] // 2:], x[..., : x.shape[-1] // 2]), dim=-1)
+
+    qr, kr = q.detach().requires_grad_(), k.detach().requires_grad_()
+    c1, s1 = cos.unsqueeze(1), sin.unsqueeze(1)
+
+    def ref_step():
+        qe = qr * c1 + rh(qr) * s1
+        ke = kr * c1 + rh(kr) * s1
+        torch.autograd.backward((qe, ke), (gq, gk))
+        qr.grad = None
+        kr.grad = None
+
+    ref_ms = timed(ref_step)
+    nbytes = R.rope_bytes(cfg.total, cfg.hq, cfg.hkv, cfg.d)
+    return {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "ref_ms": ref_ms, "bytes": nbytes,
+            "fwd_gbs": nbytes / (fwd_ms * 1e-3) / 1e9, "bwd_gbs": nbytes / (bwd_ms * 1e-3) / 1e9}
 
 
 def bench_ce(steps: int, warmup: int, chunk: int) -> dict:
@@ -207,6 +270,7 @@ def main() -> int:
     ap.add_argument("--ce-chunk", type=int, default=C.DEFAULT_CHUNK_TOKENS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-ce", action="store_true")
+    ap.add_argument("--skip-rope", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (3 times): the known-size reference that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -236,6 +300,12 @@ def main() -> int:
         ce = bench_ce(max(3, args.steps // 4), min(args.warmup, 2), args.ce_chunk)
         print(f"[bench] fused CE {ce['ms_per_step']:.3f} ms/step, {ce['tokens_per_s']:.3e} tokens/s, "
               f"{ce['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    rope = None
+    if not args.skip_rope:
+        rope = bench_rope(max(10, args.steps), args.warmup)
+        print(f"[bench] fused RoPE fwd {rope['fwd_ms'] * 1e3:.1f} us ({rope['fwd_gbs']:.0f} GB/s), bwd "
+              f"{rope['bwd_ms'] * 1e3:.1f} us ({rope['bwd_gbs']:.0f} GB/s); reference torch ops fwd+bwd "
+              f"{rope['ref_ms'] * 1e3:.1f} us", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
 
     cfg = att["cfg"]
@@ -273,6 +343,15 @@ def main() -> int:
                       "pct_bf16_peak": round(100.0 * ce["tflops"] / PEAK_BF16_TFLOPS, 2),
                       "chunk_tokens": ce["chunk"],
                       "cpu_baseline": cpu["ce"] if cpu else None}
+    if rope is not None:
+        line["rope"] = {"workload": "config-2 shape: RoPE of q [16384,12,128] and k [16384,2,128] (Qwen2 layout, "
+                                    "packed position ids), forward and backward",
+                        "fwd_us": round(rope["fwd_ms"] * 1e3, 2), "bwd_us": round(rope["bwd_ms"] * 1e3, 2),
+                        "roofline": {"bound": "hbm", "achieved": round(rope["fwd_gbs"], 1), "peak": PEAK_HBM_GBS,
+                                     "unit": "GB/s", "frac": round(rope["fwd_gbs"] / PEAK_HBM_GBS, 4),
+                                     "algorithmic_bytes": rope["bytes"]},
+                        "bwd_gbs": round(rope["bwd_gbs"], 1),
+                        "reference_torch_ops_fwd_bwd_us": round(rope["ref_ms"] * 1e3, 2)}
     if cpu:
         line["host"] = cpu["host"]
     print(json.dumps(line), flush=True)

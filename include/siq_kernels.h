@@ -1,11 +1,13 @@
 /*
  * siq_kernels.h -- C ABI of the SiQ-VL training hot path on MI355X (gfx950).
  *
- * Two operators, both hand-written HIP behind this plain-C boundary:
+ * Three operators, all hand-written HIP behind this plain-C boundary:
  *   1. varlen (cu_seqlens-packed) flash attention, forward and backward,
  *      causal GQA (Qwen2.5 decoder) or bidirectional (SigLIP tower);
  *   2. fused lm_head linear + cross-entropy, forward and backward, without
- *      materialising the [N, V] logits.
+ *      materialising the [N, V] logits;
+ *   3. the rotary position embedding of q and k that precedes attention in
+ *      the decoder, forward and backward, in one pass each.
  *
  * Conventions
  *  - Every entry point returns an int status (SIQ_OK = 0, < 0 on error) and
@@ -128,6 +130,33 @@ int siq_flce_fwd_bwd(const void* hidden, const void* weight, const int64_t* labe
  * dhidden / dweight.  Companion of siq_flce_fwd_bwd; no reference
  * counterpart (autograd's chain rule). */
 int siq_scale_bf16_inplace(void* data, int64_t numel, const float* scalar, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Rotary position embedding of q and k (Qwen2 decoder).
+ *
+ * Replaces apply_rotary_pos_emb (transformers models/qwen2/modeling_qwen2.py:
+ * 105-135, with rotate_half; called from Qwen2Attention.forward at :206-211):
+ *   q_embed = q * cos + rotate_half(q) * sin,  k_embed likewise,
+ * rotate_half(x) = cat(-x[..., D/2:], x[..., :D/2]), evaluated with the
+ * reference's bf16 rounding after every op, so the results are bitwise those
+ * of the reference's torch ops on the same bf16 inputs.  siq_rope_bwd applies
+ * the reference's autograd of the same ops to the upstream gradients
+ * (dq_embed, dk_embed) and writes dq, dk.
+ *
+ * Tensors are bf16 [batch, seqlen, heads, head_dim] (cos, sin:
+ * [batch, seqlen, head_dim]) with element strides, head_dim contiguous:
+ * strides[16] = q (b, s, h), k (b, s, h), cos (b, s), sin (b, s),
+ * q_embed (b, s, h), k_embed (b, s, h) -- for siq_rope_bwd read dq_embed,
+ * dk_embed, cos, sin, dq, dk.  Strides are multiples of 8 elements and base
+ * pointers 16-byte aligned.  An output may be its input (same pointer and
+ * strides, in place); any other overlap is undefined.  head_dim: a multiple of
+ * 16 in [16, 512].  No workspace.
+ * ------------------------------------------------------------------------- */
+int siq_rope_fwd(const void* q, const void* k, const void* cos, const void* sin, void* q_embed, void* k_embed,
+                 int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides, void* stream);
+
+int siq_rope_bwd(const void* dq_embed, const void* dk_embed, const void* cos, const void* sin, void* dq, void* dk,
+                 int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides, void* stream);
 
 #ifdef __cplusplus
 }

@@ -11,6 +11,7 @@
 #include "../../include/siq_kernels.h"
 #include "attn.h"
 #include "flce.h"
+#include "rope.h"
 
 namespace {
 
@@ -298,6 +299,78 @@ int siq_flce_fwd_bwd(const void* hidden, const void* weight, const int64_t* labe
   const hipError_t e = siq::flce_run(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "fused CE launch failed: %s", hipGetErrorString(e));
   return ok();
+}
+
+}  // extern "C"
+
+namespace {
+
+// Shared by siq_rope_fwd / siq_rope_bwd: validation, then one launch over the
+// q rows and k rows.  strides: x0 (b, s, h), x1 (b, s, h), cos (b, s),
+// sin (b, s), y0 (b, s, h), y1 (b, s, h).
+int rope_call(bool backward, const void* x0, const void* x1, const void* cosp, const void* sinp, void* y0, void* y1,
+              int64_t batch, int64_t seqlen, int hq, int hkv, int d, const int64_t* st, void* stream) {
+  const char* nm[6] = {backward ? "dq_embed" : "q", backward ? "dk_embed" : "k", "cos", "sin",
+                       backward ? "dq" : "q_embed", backward ? "dk" : "k_embed"};
+  if (batch < 0 || seqlen < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "batch and seqlen must be >= 0");
+  if (hq <= 0 || hkv <= 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "head counts must be positive (hq=%d, hkv=%d)", hq, hkv);
+  if (d < 16 || d > 512 || d % 16 != 0)
+    return fail(SIQ_ERR_UNSUPPORTED, "head_dim %d unsupported (a multiple of 16 in [16, 512])", d);
+  if (st == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "strides must not be NULL");
+  if (batch * seqlen == 0) return ok();
+  if ((batch * seqlen) > (int64_t(1) << 40)) return fail(SIQ_ERR_INVALID_ARGUMENT, "batch * seqlen too large");
+  const void* ptr[6] = {x0, x1, cosp, sinp, y0, y1};
+  const int first[6] = {0, 3, 6, 8, 10, 13}, count[6] = {3, 3, 2, 2, 3, 3};
+  for (int t = 0; t < 6; ++t) {
+    if (ptr[t] == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "%s must not be NULL", nm[t]);
+    if (!aligned16(ptr[t])) return fail(SIQ_ERR_ALIGNMENT, "%s is not 16-byte aligned", nm[t]);
+    for (int j = 0; j < count[t]; ++j) {
+      const int64_t v = st[first[t] + j];
+      if (v < 0 || (v & 7))
+        return fail(SIQ_ERR_ALIGNMENT, "%s stride %d (%lld) must be a non-negative multiple of 8 elements", nm[t], j,
+                    (long long)v);
+    }
+  }
+  auto ten = [&](int t) {
+    siq::RopeTensor r;
+    r.p = static_cast<siq::bf16*>(const_cast<void*>(ptr[t]));
+    r.sb = st[first[t]];
+    r.ss = st[first[t] + 1];
+    r.sh = count[t] == 3 ? st[first[t] + 2] : 0;
+    return r;
+  };
+  siq::RopeArgs a{};
+  a.x[0] = ten(0);
+  a.x[1] = ten(1);
+  a.cos = ten(2);
+  a.sin = ten(3);
+  a.y[0] = ten(4);
+  a.y[1] = ten(5);
+  a.batch = batch;
+  a.seqlen = seqlen;
+  a.hq = hq;
+  a.hkv = hkv;
+  a.d = d;
+  const int64_t threads = batch * seqlen * (int64_t)(hq + hkv) * (d / 16);
+  int64_t blocks = (threads + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  const hipError_t e = siq::launch_rope(a, backward, (int)blocks, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "rope launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int siq_rope_fwd(const void* q, const void* k, const void* cos, const void* sin, void* q_embed, void* k_embed,
+                 int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides, void* stream) {
+  return rope_call(false, q, k, cos, sin, q_embed, k_embed, batch, seqlen, hq, hkv, head_dim, strides, stream);
+}
+
+int siq_rope_bwd(const void* dq_embed, const void* dk_embed, const void* cos, const void* sin, void* dq, void* dk,
+                 int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides, void* stream) {
+  return rope_call(true, dq_embed, dk_embed, cos, sin, dq, dk, batch, seqlen, hq, hkv, head_dim, strides, stream);
 }
 
 int siq_scale_bf16_inplace(void* data, int64_t numel, const float* scalar, void* stream) {

@@ -1,0 +1,158 @@
+"""Fused rotary position embedding of q and k on MI355X: host side.
+
+Replaces, in the reference's Qwen2 decoder, ``apply_rotary_pos_emb``
+(transformers models/qwen2/modeling_qwen2.py:105-135 with ``rotate_half``;
+called from ``Qwen2Attention.forward`` at :206-211) by one launch of
+``siq_rope_fwd`` over q and k, and its autograd backward by one launch of
+``siq_rope_bwd``.  Results are bitwise those of the reference's bf16 torch ops
+``q * cos + rotate_half(q) * sin`` (each op rounds to bf16; the kernel repeats
+those roundings), forward and backward.
+
+Layers:
+
+* ``rope_fwd`` / ``rope_bwd`` -- raw operators on ``[batch, seqlen, heads, D]``
+  views (any strides with a contiguous ``D``).
+* ``apply_rotary_pos_emb`` -- the reference's signature (``q, k, cos, sin,
+  position_ids=None, unsqueeze_dim=1``), autograd-aware; bf16 CUDA inputs run
+  the HIP kernels, anything else (fp32 evaluation, CPU generation) takes the
+  original transformers function.
+* ``enable_fused_rope()`` -- installs it as
+  ``transformers.models.qwen2.modeling_qwen2.apply_rotary_pos_emb``, the name
+  ``Qwen2Attention.forward`` looks up at call time.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_ORIGINAL = None  # transformers' apply_rotary_pos_emb, once enable_fused_rope() has run
+
+
+def _usable(t: torch.Tensor, rank: int) -> bool:
+    if t.dim() != rank or t.stride(-1) != 1 or t.data_ptr() % 16:
+        return False
+    return all(s % 8 == 0 and s >= 0 for s in t.stride()[:-1])
+
+
+def _bshd(t: torch.Tensor, unsqueeze_dim: int) -> torch.Tensor:
+    """[batch, seqlen, heads, D] view of a q/k tensor laid out as apply_rotary_pos_emb receives it."""
+    if t.dim() != 4:
+        raise ValueError(f"q / k must be 4-D, got shape {tuple(t.shape)}")
+    if unsqueeze_dim == 1:
+        return t.transpose(1, 2)  # [B, H, S, D] -> [B, S, H, D]
+    if unsqueeze_dim == 2:
+        return t
+    raise ValueError(f"unsqueeze_dim must be 1 ([B, H, S, D]) or 2 ([B, S, H, D]), got {unsqueeze_dim}")
+
+
+def _prep(t: torch.Tensor, rank: int) -> torch.Tensor:
+    return t if _usable(t, rank) else t.contiguous()
+
+
+def _launch(fn_name: str, x0, x1, cos, sin, y0, y1) -> None:
+    b, s, hq, d = x0.shape
+    hkv = x1.shape[2]
+    strides = [*x0.stride()[:3], *x1.stride()[:3], *cos.stride()[:2], *sin.stride()[:2], *y0.stride()[:3],
+               *y1.stride()[:3]]
+    stream = torch.cuda.current_stream(x0.device).cuda_stream
+    rc = getattr(_lib.lib(), fn_name)(x0.data_ptr(), x1.data_ptr(), cos.data_ptr(), sin.data_ptr(), y0.data_ptr(),
+                                      y1.data_ptr(), b, s, hq, hkv, d, _lib.int64_array(strides), stream)
+    _lib.check(rc, fn_name)
+
+
+def _check(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> None:
+    for name, t in (("q", q), ("k", k), ("cos", cos), ("sin", sin)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+        if t.device.type != "cuda":
+            raise ValueError(f"{name} must live on the GPU, got {t.device}")
+    b, s, _, d = q.shape
+    if k.shape[0] != b or k.shape[1] != s or k.shape[3] != d:
+        raise ValueError(f"k {tuple(k.shape)} does not match q {tuple(q.shape)} in batch / seqlen / head_dim")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dim() != 3 or t.shape[1] != s or t.shape[2] != d or t.shape[0] not in (1, b):
+            raise ValueError(f"{name} must be [batch or 1, seqlen, head_dim] = [{b}, {s}, {d}], got {tuple(t.shape)}")
+
+
+def _expand_cs(t: torch.Tensor, b: int) -> torch.Tensor:
+    return t.expand(b, -1, -1) if t.shape[0] != b else t
+
+
+def rope_fwd(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+    """Raw forward on ``[B, S, H, D]`` views; returns ``(q_embed, k_embed)`` laid out like q and k."""
+    _check(q, k, cos, sin)
+    q, k = _prep(q, 4), _prep(k, 4)
+    cos, sin = _prep(_expand_cs(cos, q.shape[0]), 3), _prep(_expand_cs(sin, q.shape[0]), 3)
+    qe, ke = torch.empty_like(q), torch.empty_like(k)
+    if q.numel() and k.numel():
+        _launch("siq_rope_fwd", q, k, cos, sin, qe, ke)
+    return qe, ke
+
+
+def rope_bwd(dq_embed: torch.Tensor, dk_embed: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+    """Raw backward on ``[B, S, H, D]`` views; returns ``(dq, dk)``."""
+    _check(dq_embed, dk_embed, cos, sin)
+    g0, g1 = _prep(dq_embed, 4), _prep(dk_embed, 4)
+    cos, sin = _prep(_expand_cs(cos, g0.shape[0]), 3), _prep(_expand_cs(sin, g0.shape[0]), 3)
+    dq, dk = torch.empty_like(g0), torch.empty_like(g1)
+    if g0.numel() and g1.numel():
+        _launch("siq_rope_bwd", g0, g1, cos, sin, dq, dk)
+    return dq, dk
+
+
+class _Rope(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, cos, sin, unsqueeze_dim):
+        if cos.requires_grad or sin.requires_grad:
+            raise ValueError("gradients with respect to cos / sin are not supported")
+        qe, ke = rope_fwd(_bshd(q, unsqueeze_dim), _bshd(k, unsqueeze_dim), cos, sin)
+        ctx.save_for_backward(cos, sin)
+        ctx.unsqueeze_dim = unsqueeze_dim
+        return _bshd(qe, unsqueeze_dim), _bshd(ke, unsqueeze_dim)
+
+    @staticmethod
+    def backward(ctx, dqe, dke):
+        cos, sin = ctx.saved_tensors
+        u = ctx.unsqueeze_dim
+        dq, dk = rope_bwd(_bshd(dqe, u), _bshd(dke, u), cos, sin)
+        return _bshd(dq, u), _bshd(dk, u), None, None, None
+
+
+def apply_rotary_pos_emb(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, position_ids=None,
+                         unsqueeze_dim: int = 1):
+    """Signature of transformers' ``apply_rotary_pos_emb`` (``position_ids`` is unused there too)."""
+    del position_ids
+    if all(t.is_cuda and t.dtype == torch.bfloat16 for t in (q, k, cos, sin)):
+        return _Rope.apply(q, k, cos, sin, unsqueeze_dim)
+    if _ORIGINAL is None:
+        raise ValueError("the fused RoPE takes bf16 CUDA tensors (enable_fused_rope() keeps the original for others)")
+    return _ORIGINAL(q, k, cos, sin, unsqueeze_dim=unsqueeze_dim)
+
+
+def enable_fused_rope() -> None:
+    """Makes every Qwen2 attention layer call the fused RoPE (idempotent)."""
+    global _ORIGINAL
+    from transformers.models.qwen2 import modeling_qwen2 as m
+
+    if m.apply_rotary_pos_emb is apply_rotary_pos_emb:
+        return
+    _ORIGINAL = m.apply_rotary_pos_emb
+    m.apply_rotary_pos_emb = apply_rotary_pos_emb
+
+
+def disable_fused_rope() -> None:
+    """Restores transformers' own apply_rotary_pos_emb."""
+    global _ORIGINAL
+    from transformers.models.qwen2 import modeling_qwen2 as m
+
+    if _ORIGINAL is not None and m.apply_rotary_pos_emb is apply_rotary_pos_emb:
+        m.apply_rotary_pos_emb = _ORIGINAL
+    _ORIGINAL = None
+
+
+def rope_bytes(tokens: int, hq: int, hkv: int, d: int) -> int:
+    """Algorithmic HBM bytes of one pass (forward or backward): q and k read and
+    written once, plus one cos and one sin row per token."""
+    return tokens * (2 * (hq + hkv) * d * 2 + 2 * d * 2)

@@ -166,3 +166,46 @@ def test_ctypes_prototypes_cover_header_arity():
         assert m, name
         params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
         assert len(params) == len(args), (name, len(params), len(args))
+
+
+def _rope(lib, fwd=True, **kw):
+    args = dict(x0=FAKE, x1=FAKE, cos=FAKE, sin=FAKE, y0=FAKE, y1=FAKE, batch=1, seqlen=8, hq=4, hkv=2, d=128,
+                strides=_strides(16), stream=None)
+    args.update(kw)
+    fn = lib.siq_rope_fwd if fwd else lib.siq_rope_bwd
+    return fn(*args.values())
+
+
+@pytest.mark.parametrize("fwd", [True, False])
+@pytest.mark.parametrize("kw,code", [
+    (dict(d=72), _lib.SIQ_ERR_UNSUPPORTED),
+    (dict(d=0), _lib.SIQ_ERR_UNSUPPORTED),
+    (dict(d=1024), _lib.SIQ_ERR_UNSUPPORTED),
+    (dict(hq=0), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(hkv=-1), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(batch=-1), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(seqlen=-3), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(strides=None), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(cos=None), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(y1=None), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(x0=FAKE + 8), _lib.SIQ_ERR_ALIGNMENT),
+    (dict(sin=FAKE + 4), _lib.SIQ_ERR_ALIGNMENT),
+])
+def test_rope_validation(lib, fwd, kw, code):
+    assert _rope(lib, fwd, **kw) == code
+    assert lib.siq_last_error().decode()
+
+
+@pytest.mark.parametrize("pos", [0, 5, 7, 15])
+def test_rope_odd_strides_rejected(lib, pos):
+    st = [128] * 16
+    st[pos] = 132
+    assert _rope(lib, strides=_lib.int64_array(st)) == _lib.SIQ_ERR_ALIGNMENT
+    st[pos] = -128
+    assert _rope(lib, strides=_lib.int64_array(st)) == _lib.SIQ_ERR_ALIGNMENT
+
+
+def test_rope_empty_is_a_no_op(lib):
+    # nothing to rotate: returns before touching the device (pointers are never read)
+    assert _rope(lib, seqlen=0) == _lib.SIQ_OK
+    assert _rope(lib, False, batch=0) == _lib.SIQ_OK
