@@ -150,7 +150,8 @@ int siq_scale_bf16_inplace(void* data, int64_t numel, const float* scalar, void*
  * dk_embed, cos, sin, dq, dk.  Strides are multiples of 8 elements and base
  * pointers 16-byte aligned.  An output may be its input (same pointer and
  * strides, in place); any other overlap is undefined.  head_dim: a multiple of
- * 16 in [16, 512].  No workspace.
+ * 16 in [16, 512]; hq, hkv <= 4096; batch * seqlen < 2^32.
+ * No workspace.
  * ------------------------------------------------------------------------- */
 int siq_rope_fwd(const void* q, const void* k, const void* cos, const void* sin, void* q_embed, void* k_embed,
                  int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides, void* stream);

@@ -313,12 +313,14 @@ int rope_call(bool backward, const void* x0, const void* x1, const void* cosp, c
   const char* nm[6] = {backward ? "dq_embed" : "q", backward ? "dk_embed" : "k", "cos", "sin",
                        backward ? "dq" : "q_embed", backward ? "dk" : "k_embed"};
   if (batch < 0 || seqlen < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "batch and seqlen must be >= 0");
-  if (hq <= 0 || hkv <= 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "head counts must be positive (hq=%d, hkv=%d)", hq, hkv);
+  if (hq <= 0 || hkv <= 0 || hq > 4096 || hkv > 4096)
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "head counts must be in [1, 4096] (hq=%d, hkv=%d)", hq, hkv);
   if (d < 16 || d > 512 || d % 16 != 0)
     return fail(SIQ_ERR_UNSUPPORTED, "head_dim %d unsupported (a multiple of 16 in [16, 512])", d);
   if (st == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "strides must not be NULL");
   if (batch * seqlen == 0) return ok();
-  if ((batch * seqlen) > (int64_t(1) << 40)) return fail(SIQ_ERR_INVALID_ARGUMENT, "batch * seqlen too large");
+  if (batch * seqlen >= (int64_t(1) << 32) || batch >= (int64_t(1) << 31) || seqlen >= (int64_t(1) << 31))
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "batch * seqlen must be < 2^32");
   const void* ptr[6] = {x0, x1, cosp, sinp, y0, y1};
   const int first[6] = {0, 3, 6, 8, 10, 13}, count[6] = {3, 3, 2, 2, 3, 3};
   for (int t = 0; t < 6; ++t) {
@@ -351,10 +353,7 @@ int rope_call(bool backward, const void* x0, const void* x1, const void* cosp, c
   a.hq = hq;
   a.hkv = hkv;
   a.d = d;
-  const int64_t threads = batch * seqlen * (int64_t)(hq + hkv) * (d / 16);
-  int64_t blocks = (threads + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  const hipError_t e = siq::launch_rope(a, backward, (int)blocks, static_cast<hipStream_t>(stream));
+  const hipError_t e = siq::launch_rope(a, backward, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "rope launch failed: %s", hipGetErrorString(e));
   return ok();
 }

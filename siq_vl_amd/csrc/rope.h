@@ -22,6 +22,7 @@ struct RopeArgs {
   int hq, hkv, d;
 };
 
-hipError_t launch_rope(const RopeArgs& a, bool backward, int blocks, hipStream_t stream);
+// Needs d a multiple of 16 in [16, 512] and batch * seqlen < 2^32.
+hipError_t launch_rope(const RopeArgs& a, bool backward, hipStream_t stream);
 
 }  // namespace siq

@@ -21,11 +21,14 @@
 // HBM-bound, 2 * (Hq + Hkv) * D * 2 bytes per token plus the cos / sin rows
 // (L2 hits after the first head of a token).
 //
-// Work split: one thread per (row, 8-element chunk of the first half), row =
-// (batch b, position s, head h) of q or k; the thread loads its chunk and the
-// matching chunk of the second half (two 16-byte loads), and the cos / sin
-// chunks of both halves, and writes both output chunks.  Consecutive threads
-// take consecutive chunks of one row, so a wave covers whole rows.
+// Work split: a thread owns one 8-element chunk c of the first half (and the
+// matching chunk of the second) of one token at a time: D / 16 threads per
+// token, 256 / (D / 16) tokens per block step, blocks striding over tokens
+// (batch b, position s).  The thread loads its token's cos / sin chunks once
+// and applies them to every q and k head of the token (two 16-byte loads and
+// two 16-byte stores per head); a wave covers the same head of several
+// tokens, whole 2 D-byte rows each.  Index arithmetic is one 32-bit division
+// per token.
 #include "rope.h"
 
 namespace siq {
@@ -43,50 +46,59 @@ __device__ __forceinline__ float rbf(float x) {
 }
 
 template <bool BWD>
+__device__ __forceinline__ void rope_row(const bf16* src, bf16* dst, int half, const bf16x8& c1, const bf16x8& c2,
+                                         const bf16x8& s1, const bf16x8& s2) {
+  const bf16x8 x1 = ld_bf16x8(src), x2 = ld_bf16x8(src + half);
+  bf16x8 o1, o2;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float u = (float)x1[k], v = (float)x2[k];
+    if (!BWD) {
+      o1[k] = (bf16)(rbf(u * (float)c1[k]) + rbf(-v * (float)s1[k]));
+      o2[k] = (bf16)(rbf(v * (float)c2[k]) + rbf(u * (float)s2[k]));
+    } else {
+      o1[k] = (bf16)(rbf(u * (float)c1[k]) + rbf(v * (float)s2[k]));
+      o2[k] = (bf16)(rbf(v * (float)c2[k]) - rbf(u * (float)s1[k]));
+    }
+  }
+  st_bf16x8(dst, o1);
+  st_bf16x8(dst + half, o2);
+}
+
+template <bool BWD>
 __global__ __launch_bounds__(256) void rope_kernel(const RopeArgs a) {
-  const int cph = a.d / 16;  // chunks per half row
-  const int64_t qrows = a.batch * a.seqlen * a.hq;
-  const int64_t rows = qrows + a.batch * a.seqlen * a.hkv;
-  const int64_t total = rows * cph;
+  const int cph = a.d / 16;          // chunks per half row (threads per token)
+  const int tpb = 256 / cph;         // tokens per block step
+  const int t = threadIdx.x;
+  if (t >= tpb * cph) return;  // 256 not a multiple of D / 16
+  const int c = t % cph;
   const int half = a.d / 2;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t row = i / cph;
-    const int c = (int)(i - row * cph);
-    const bool isq = row < qrows;
-    const int64_t r = isq ? row : row - qrows;
-    const int H = isq ? a.hq : a.hkv;
-    const int64_t bs = r / H;
-    const int h = (int)(r - bs * H);
-    const int64_t b = bs / a.seqlen, s = bs - b * a.seqlen;
-    const RopeTensor& xin = isq ? a.x[0] : a.x[1];
-    const RopeTensor& xout = isq ? a.y[0] : a.y[1];
-    const bf16* src = xin.p + b * xin.sb + s * xin.ss + h * xin.sh + 8 * c;
-    bf16* dst = xout.p + b * xout.sb + s * xout.ss + h * xout.sh + 8 * c;
+  const uint32_t S = (uint32_t)a.seqlen;
+  const uint32_t ntok = (uint32_t)(a.batch * a.seqlen);
+  for (uint32_t tok = blockIdx.x * tpb + t / cph; tok < ntok; tok += gridDim.x * tpb) {
+    const uint32_t b = tok / S, s = tok - b * S;
     const bf16* cp = a.cos.p + b * a.cos.sb + s * a.cos.ss + 8 * c;
     const bf16* sp = a.sin.p + b * a.sin.sb + s * a.sin.ss + 8 * c;
-    const bf16x8 x1 = ld_bf16x8(src), x2 = ld_bf16x8(src + half);
     const bf16x8 c1 = ld_bf16x8(cp), c2 = ld_bf16x8(cp + half);
     const bf16x8 s1 = ld_bf16x8(sp), s2 = ld_bf16x8(sp + half);
-    bf16x8 o1, o2;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float u = (float)x1[k], v = (float)x2[k];
-      if (!BWD) {
-        o1[k] = (bf16)(rbf(u * (float)c1[k]) + rbf(-v * (float)s1[k]));
-        o2[k] = (bf16)(rbf(v * (float)c2[k]) + rbf(u * (float)s2[k]));
-      } else {
-        o1[k] = (bf16)(rbf(u * (float)c1[k]) + rbf(v * (float)s2[k]));
-        o2[k] = (bf16)(rbf(v * (float)c2[k]) - rbf(u * (float)s1[k]));
-      }
-    }
-    st_bf16x8(dst, o1);
-    st_bf16x8(dst + half, o2);
+#pragma unroll 2
+    for (int h = 0; h < a.hq; ++h)
+      rope_row<BWD>(a.x[0].p + b * a.x[0].sb + s * a.x[0].ss + h * a.x[0].sh + 8 * c,
+                    a.y[0].p + b * a.y[0].sb + s * a.y[0].ss + h * a.y[0].sh + 8 * c, half, c1, c2, s1, s2);
+#pragma unroll 2
+    for (int h = 0; h < a.hkv; ++h)
+      rope_row<BWD>(a.x[1].p + b * a.x[1].sb + s * a.x[1].ss + h * a.x[1].sh + 8 * c,
+                    a.y[1].p + b * a.y[1].sb + s * a.y[1].ss + h * a.y[1].sh + 8 * c, half, c1, c2, s1, s2);
   }
 }
 
 }  // namespace
 
-hipError_t launch_rope(const RopeArgs& a, bool backward, int blocks, hipStream_t stream) {
+hipError_t launch_rope(const RopeArgs& a, bool backward, hipStream_t stream) {
+  const int64_t tpb = 256 / (a.d / 16);  // tokens per block step
+  const int64_t ntok = a.batch * a.seqlen;
+  int64_t blocks = (ntok + tpb - 1) / tpb;
+  if (blocks > 2048) blocks = 2048;
   if (backward)
     hipLaunchKernelGGL(rope_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
   else

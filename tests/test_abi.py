@@ -183,6 +183,8 @@ def _rope(lib, fwd=True, **kw):
     (dict(d=1024), _lib.SIQ_ERR_UNSUPPORTED),
     (dict(hq=0), _lib.SIQ_ERR_INVALID_ARGUMENT),
     (dict(hkv=-1), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(hq=5000), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(batch=1 << 20, seqlen=1 << 12), _lib.SIQ_ERR_INVALID_ARGUMENT),
     (dict(batch=-1), _lib.SIQ_ERR_INVALID_ARGUMENT),
     (dict(seqlen=-3), _lib.SIQ_ERR_INVALID_ARGUMENT),
     (dict(strides=None), _lib.SIQ_ERR_INVALID_ARGUMENT),

@@ -190,3 +190,23 @@ def test_dropin_qwen2_bitwise():
         # the embedding gradient is an atomic scatter-add: not bitwise repeatable on its own
         if "embed_tokens" not in n:
             assert same(grads[n], ref_grads[n]), n
+
+
+@pytest.mark.parametrize("d", [16, 48, 80])
+def test_other_head_dims_bitwise(d):
+    # chunk counts that are not powers of two (and leave block threads idle)
+    print(f"rope d={d}", flush=True)
+    q, k, cos, sin = make(2, 45, 5, 3, d, seed=7)
+    qe, ke = R.apply_rotary_pos_emb(q, k, cos, sin)
+    rq, rk = torch_rope(q, k, cos, sin)
+    assert same(qe, rq) and same(ke, rk)
+
+
+def test_in_place_through_the_abi():
+    print("rope in place", flush=True)
+    q, k, cos, sin = make(2, 33, 4, 2, 128, seed=8)
+    rq, rk = torch_rope(q, k, cos, sin)
+    bq = R._bshd(q, 1).contiguous()
+    bk = R._bshd(k, 1).contiguous()
+    R._launch("siq_rope_fwd", bq, bk, cos, sin, bq, bk)  # outputs are the inputs
+    assert same(bq, R._bshd(rq, 1)) and same(bk, R._bshd(rk, 1))
