@@ -313,6 +313,18 @@ __global__ __launch_bounds__(NT) void flce_logits_kernel(const LogitsArgs p) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int wi = w & 1, wj = w >> 1;
   float* red = reinterpret_cast<float*>(smem);  // [2][256]
+  // accumulator (a, b, r) holds z for vocab row vbase + 32 a + 16 (r / 8) + (r % 8) and token column
+  // j0 + 64 wj + 32 b + l32.  Only the last vocab tile has rows past V: masked there alone.
+  const int64_t vbase = i0 + 128 * wi + 8 * h;
+  if (i0 + BI > p.V) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (vbase + 32 * a + 16 * (r >> 3) + (r & 7) >= p.V) acc[a][b][r] = -INFINITY;
+  }
   float mt[2];
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
@@ -320,13 +332,9 @@ __global__ __launch_bounds__(NT) void flce_logits_kernel(const LogitsArgs p) {
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t v = i0 + 128 * wi + 32 * a + drow(r, h);
-        const float z2 = v < p.V ? acc[a][b][r] * kLog2e : -INFINITY;
-        acc[a][b][r] = z2;
-        mx = fmaxf(mx, z2);
-      }
-    mx = wave_max_xor32(mx);
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc[a][b][r]);
+    // tile max in log2 units (scaling by log2 e > 0 commutes with the max)
+    mx = wave_max_xor32(mx) * kLog2e;
     if (h == 0) red[wi * 256 + 64 * wj + 32 * b + l32] = mx;
   }
   __syncthreads();
@@ -341,27 +349,39 @@ __global__ __launch_bounds__(NT) void flce_logits_kernel(const LogitsArgs p) {
     const int col = 64 * wj + 32 * b + l32;
     const int64_t tok = j0 + col;
     const bool tv = tok < p.nc;
-    const int64_t yv = tv ? p.y[tok] : -1;
-    float s = 0.f;
+    // the label logit: held by at most one lane of the workgroup, for one
+    // vocab tile in ~600 -- located with one range test per token
+    const int64_t rel64 = (tv ? p.y[tok] : -1) - vbase;
+    const bool hit = rel64 >= 0 && rel64 < 128 && ((rel64 >> 3) & 1) == 0;
+    if (__any(hit)) {
+      const int rel = (int)rel64;
+      float zsel = 0.f;
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (hit && rel == 32 * a + 16 * (r >> 3) + (r & 7)) zsel = acc[a][b][r];
+      if (hit) p.zy[tok] = zsel;
+    }
+    const float m2 = mt[b];
+    float sum = 0.f;
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        const int64_t v0 = i0 + 128 * wi + 32 * a + 16 * jj + 8 * h;
+        const int64_t v0 = vbase + 32 * a + 16 * jj;
         bf16x8 e8;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float z2 = acc[a][b][8 * jj + i];
-          const float e = exp2f_fast(z2 - mt[b]);
-          s += e;
+          const float e = exp2f_fast(__builtin_fmaf(acc[a][b][8 * jj + i], kLog2e, -m2));
+          sum += e;
           e8[i] = (bf16)e;
-          if (v0 + i == yv) p.zy[tok] = z2 * kLn2;
         }
         if (tv && v0 < p.V) st_bf16x8(p.E + tok * p.V + v0, e8);
       }
     }
-    s = wave_sum_xor32(s);
-    if (h == 0) red[wi * 256 + col] = s;
+    sum = wave_sum_xor32(sum);
+    if (h == 0) red[wi * 256 + col] = sum;
   }
   __syncthreads();
   if (wi == 0 && h == 0) {
@@ -411,21 +431,40 @@ __global__ __launch_bounds__(256) void flce_row_kernel(const RowArgs p) {
   const bool valid = yv != p.ignore_index && yv >= 0 && yv < p.V;
   const float gv = valid ? *p.invden : 0.f;
   if (lane == 0) p.loss_row[row] = valid ? lse2 * kLn2 - p.zy[row] : 0.f;
-  // dZ, 8 columns per lane per step (V is a multiple of 8, so a chunk never
-  // straddles the row end; 8 aligned columns never straddle a 256-column tile)
+  // dZ, 8 columns per lane per chunk (V is a multiple of 8, so a chunk never
+  // straddles the row end; 8 aligned columns never straddle a 256-column
+  // tile).  An ignored row's dZ is zero: written without reading E.
   bf16* e = p.E + row * p.V;
-  for (int64_t v0 = 8 * (int64_t)lane; v0 < p.V; v0 += 512) {
-    const float fv = exp2f_fast(m[v0 / kVT] - lse2) * gv;
-    const bf16x8 x = ld_bf16x8(e + v0);
-    bf16x8 o;
+  const int64_t nchunk = p.V / 8;
+  if (gv == 0.f) {
+    for (int64_t c = lane; c < nchunk; c += 64) st_bf16x8(e + 8 * c, zero_bf16x8());
+    return;
+  }
+  // U chunks per lane in flight: one 16-byte load at a time leaves the pass latency-bound
+  constexpr int U = 8;
+  for (int64_t c0 = lane; c0 < nchunk; c0 += 64 * U) {
+    bf16x8 x[U];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (bf16)((float)x[i] * fv);
-    const int64_t yrel = yv - v0;
-    if (valid && yrel >= 0 && yrel < 8) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (i == yrel) ? (bf16)((float)x[i] * fv - gv) : o[i];
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + 64 * u;
+      x[u] = c < nchunk ? ld_bf16x8(e + 8 * c) : zero_bf16x8();
     }
-    st_bf16x8(e + v0, o);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + 64 * u;
+      if (c >= nchunk) break;
+      const int64_t v0 = 8 * c;
+      const float fv = exp2f_fast(m[v0 / kVT] - lse2) * gv;
+      bf16x8 o;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = (bf16)((float)x[u][i] * fv);
+      const int64_t yrel = yv - v0;
+      if (yrel >= 0 && yrel < 8) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = (i == yrel) ? (bf16)((float)x[u][i] * fv - gv) : o[i];
+      }
+      st_bf16x8(e + v0, o);
+    }
   }
 }
 
