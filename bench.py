@@ -31,6 +31,7 @@ import torch
 
 from siq_vl_amd import attention as A
 from siq_vl_amd import cross_entropy as C
+from siq_vl_amd import projector as PJ
 from siq_vl_amd import rope as R
 from siq_vl_amd import workloads as W
 
@@ -186,6 +187,60 @@ def bench_rope(steps: int, warmup: int) -> dict:
             "fwd_gbs": nbytes / (fwd_ms * 1e-3) / 1e9, "bwd_gbs": nbytes / (bwd_ms * 1e-3) / 1e9}
 
 
+def bench_projector(steps: int, warmup: int) -> dict:
+    """Pixel-shuffle projector forward + backward (dx and dweight) at the production
+    shape: 16 SigLIP2-large-512 tiles (32 x 32 patches x 1024) -> Qwen2.5-1.5B (1536),
+    r = 2; the reference's torch ops (modeling.py:74-105 and their autograd) beside it."""
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(W.SEED)
+    batch, side, dv, r, n = 16, 32, 1024, 2, 1536
+    x = torch.randn(batch, side * side, dv, generator=g).to(torch.bfloat16).to(dev)
+    w = (0.02 * torch.randn(n, dv * r * r, generator=g)).to(torch.bfloat16).to(dev)
+    dy = torch.randn(batch, (side // r) ** 2, n, generator=g).to(torch.bfloat16).to(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn, reps):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ev = _events(steps + 1)
+        ev[0].record(stream)
+        for i in range(steps):
+            fn()
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+        return per[len(per) // 2] / reps
+
+    def graphed(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(reps):
+                fn()
+        return timed(gr.replay, reps)
+
+    fwd_ms = graphed(lambda: PJ.proj_fwd(x, w, r))
+    bwd_ms = graphed(lambda: PJ.proj_bwd(x, w, dy, r))
+    xr, wr = x.detach().requires_grad_(), w.detach().requires_grad_()
+
+    def ref_step():
+        xs = xr.view(batch, side, side, dv).reshape(batch, side // r, r, side // r, r, dv)
+        xs = xs.permute(0, 1, 3, 2, 4, 5).contiguous().reshape(batch, (side // r) ** 2, dv * r * r)
+        torch.nn.functional.linear(xs, wr).backward(dy)
+        xr.grad = None
+        wr.grad = None
+
+    ref_ms = timed(ref_step, 1)
+    m, k = batch * (side // r) ** 2, dv * r * r
+    fl_f, fl_b = PJ.projector_flops(m, k, n, backward=False), PJ.projector_flops(m, k, n) - PJ.projector_flops(
+        m, k, n, backward=False)
+    return {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "ref_ms": ref_ms, "m": m, "k": k, "n": n,
+            "tflops": (fl_f + fl_b) / ((fwd_ms + bwd_ms) * 1e-3) / 1e12,
+            "fwd_tflops": fl_f / (fwd_ms * 1e-3) / 1e12, "bwd_tflops": fl_b / (bwd_ms * 1e-3) / 1e12}
+
+
 def bench_ce(steps: int, warmup: int, chunk: int) -> dict:
     cfg = W.CONFIG4
     dev = torch.device("cuda")
@@ -284,6 +339,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-ce", action="store_true")
     ap.add_argument("--skip-rope", action="store_true")
+    ap.add_argument("--skip-projector", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (3 times): the known-size reference that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -320,6 +376,12 @@ def main() -> int:
               f"{rope['bwd_ms'] * 1e3:.1f} us ({rope['bwd_gbs']:.0f} GB/s) in a graph; one eager call "
               f"{rope['eager_fwd_ms'] * 1e3:.1f} us; reference torch ops fwd+bwd {rope['ref_ms'] * 1e3:.1f} us",
               file=sys.stderr, flush=True)
+    proj = None
+    if not args.skip_projector:
+        proj = bench_projector(max(10, args.steps), args.warmup)
+        print(f"[bench] projector fwd {proj['fwd_ms'] * 1e3:.1f} us ({proj['fwd_tflops']:.0f} TFLOP/s), bwd "
+              f"{proj['bwd_ms'] * 1e3:.1f} us ({proj['bwd_tflops']:.0f} TFLOP/s); reference torch ops fwd+bwd "
+              f"{proj['ref_ms'] * 1e3:.1f} us", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
 
     cfg = att["cfg"]
@@ -368,6 +430,15 @@ def main() -> int:
                                      "algorithmic_bytes": rope["bytes"]},
                         "bwd_gbs": round(rope["bwd_gbs"], 1),
                         "reference_torch_ops_fwd_bwd_us": round(rope["ref_ms"] * 1e3, 2)}
+    if proj is not None:
+        line["projector"] = {
+            "workload": "pixel-shuffle projector fwd+bwd (dx, dweight): 16 tiles x 32x32 patches x 1024 -> r 2 -> "
+                        "[4096 tokens, 4096] x [1536, 4096]^T",
+            "fwd_us": round(proj["fwd_ms"] * 1e3, 2), "bwd_us": round(proj["bwd_ms"] * 1e3, 2),
+            "timing": "5 launches captured in a HIP graph, replayed; events on the launch stream",
+            "roofline": {"bound": "mfma", "achieved": round(proj["tflops"], 1), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(proj["tflops"] / PEAK_BF16_TFLOPS, 4)},
+            "reference_torch_ops_fwd_bwd_us": round(proj["ref_ms"] * 1e3, 2)}
     if cpu:
         line["host"] = cpu["host"]
     print(json.dumps(line), flush=True)

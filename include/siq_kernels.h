@@ -1,13 +1,15 @@
 /*
  * siq_kernels.h -- C ABI of the SiQ-VL training hot path on MI355X (gfx950).
  *
- * Three operators, all hand-written HIP behind this plain-C boundary:
+ * Four operators, all hand-written HIP behind this plain-C boundary:
  *   1. varlen (cu_seqlens-packed) flash attention, forward and backward,
  *      causal GQA (Qwen2.5 decoder) or bidirectional (SigLIP tower);
  *   2. fused lm_head linear + cross-entropy, forward and backward, without
  *      materialising the [N, V] logits;
  *   3. the rotary position embedding of q and k that precedes attention in
- *      the decoder, forward and backward, in one pass each.
+ *      the decoder, forward and backward, in one pass each;
+ *   4. the pixel-shuffle projector (vision features to text embeddings),
+ *      forward and backward, with the shuffle folded into the GEMM loads.
  *
  * Conventions
  *  - Every entry point returns an int status (SIQ_OK = 0, < 0 on error) and
@@ -158,6 +160,32 @@ int siq_rope_fwd(const void* q, const void* k, const void* cos, const void* sin,
 
 int siq_rope_bwd(const void* dq_embed, const void* dk_embed, const void* cos, const void* sin, void* dq, void* dk,
                  int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Pixel-shuffle projector (the vision-to-text bridge).
+ *
+ * Replaces SiQ_VLProjector.forward (siq_vl/model/modeling.py:100-105): the
+ * pixel shuffle of :74-98 (view [batch, side, side, dv], reshape by the
+ * factor r, permute(0, 1, 3, 2, 4, 5), reshape to [batch, (side/r)^2,
+ * r*r*dv]) followed by the bias-free Linear mlp (:59) -- and its autograd
+ * backward -- without materialising the shuffled tensor:
+ *   y [batch*(side/r)^2, out_features] = shuffle(x) weight^T,
+ *   dx = unshuffle(dy weight),  dweight = dy^T shuffle(x).
+ * x [batch, side*side, vision_dim], weight [out_features, r*r*vision_dim],
+ * y / dy [batch*(side/r)^2, out_features]: bf16, contiguous, 16-byte
+ * aligned; fp32 accumulation.  vision_dim % 64 == 0, out_features % 8 == 0,
+ * side % r == 0; x, y and weight each < 2^31 elements, tokens < 2^24.
+ * siq_proj_bwd: dx and/or dweight may be NULL (not computed).  Workspace:
+ * siq_proj_workspace_bytes (split-K partial sums; may be 0).  Deterministic.
+ * ------------------------------------------------------------------------- */
+size_t siq_proj_workspace_bytes(int64_t batch, int64_t side, int64_t vision_dim, int factor, int64_t out_features);
+
+int siq_proj_fwd(const void* x, const void* weight, void* y, int64_t batch, int64_t side, int64_t vision_dim,
+                 int factor, int64_t out_features, void* workspace, size_t workspace_bytes, void* stream);
+
+int siq_proj_bwd(const void* x, const void* weight, const void* dy, void* dx, void* dweight, int64_t batch,
+                 int64_t side, int64_t vision_dim, int factor, int64_t out_features, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

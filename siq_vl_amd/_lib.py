@@ -52,6 +52,11 @@ _PROTOS = {
          _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _size, _c_void_p],
     ),
     "siq_scale_bf16_inplace": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p]),
+    "siq_proj_workspace_bytes": (_size, [_i64, _i64, _i64, _i32, _i64]),
+    "siq_proj_fwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _i64, _c_void_p, _size,
+                            _c_void_p]),
+    "siq_proj_bwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _i64,
+                            _c_void_p, _size, _c_void_p]),
     "siq_rope_fwd": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32, _i32, _i32,

@@ -11,6 +11,7 @@
 #include "../../include/siq_kernels.h"
 #include "attn.h"
 #include "flce.h"
+#include "proj.h"
 #include "rope.h"
 
 namespace {
@@ -370,6 +371,93 @@ int siq_rope_fwd(const void* q, const void* k, const void* cos, const void* sin,
 int siq_rope_bwd(const void* dq_embed, const void* dk_embed, const void* cos, const void* sin, void* dq, void* dk,
                  int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides, void* stream) {
   return rope_call(true, dq_embed, dk_embed, cos, sin, dq, dk, batch, seqlen, hq, hkv, head_dim, strides, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Geometry checks shared by the projector entry points.
+int check_proj(int64_t batch, int64_t side, int64_t dv, int r, int64_t n) {
+  if (batch < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "batch must be >= 0");
+  if (side <= 0 || r <= 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "side and factor must be positive");
+  if (side % r != 0)
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "side %lld is not divisible by the pixel-shuffle factor %d", (long long)side, r);
+  if (dv <= 0 || dv % 64 != 0) return fail(SIQ_ERR_UNSUPPORTED, "vision_dim %lld must be a positive multiple of 64", (long long)dv);
+  if (n <= 0 || n % 8 != 0) return fail(SIQ_ERR_UNSUPPORTED, "out_features %lld must be a positive multiple of 8", (long long)n);
+  const int64_t k = (int64_t)r * r * dv, m = batch * (side / r) * (side / r);
+  if (batch * side * side * dv >= (int64_t(1) << 31) || m >= (int64_t(1) << 24) || k * n >= (int64_t(1) << 31) ||
+      m * n >= (int64_t(1) << 31))
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "projector sizes too large (x, y and weight must each hold < 2^31 elements, "
+                "tokens < 2^24)");
+  return SIQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t siq_proj_workspace_bytes(int64_t batch, int64_t side, int64_t vision_dim, int factor, int64_t out_features) {
+  if (check_proj(batch, side, vision_dim, factor, out_features) != SIQ_OK) return 0;
+  return siq::proj_workspace_bytes(batch, side, vision_dim, factor, out_features);
+}
+
+int siq_proj_fwd(const void* x, const void* weight, void* y, int64_t batch, int64_t side, int64_t vision_dim,
+                 int factor, int64_t out_features, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_proj(batch, side, vision_dim, factor, out_features);
+  if (rc) return rc;
+  if (weight == nullptr || !aligned16(weight)) return fail(SIQ_ERR_ALIGNMENT, "weight must be non-NULL and 16-byte aligned");
+  if (batch == 0) return ok();
+  if (x == nullptr || y == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "x and y must not be NULL");
+  if (!aligned16(x) || !aligned16(y)) return fail(SIQ_ERR_ALIGNMENT, "x / y not 16-byte aligned");
+  const size_t need = siq::proj_workspace_bytes(batch, side, vision_dim, factor, out_features);
+  if (need > 0 && (ws == nullptr || ws_bytes < need || !aligned16(ws)))
+    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
+  siq::ProjArgs a{};
+  a.x = static_cast<const siq::bf16*>(x);
+  a.weight = static_cast<const siq::bf16*>(weight);
+  a.y = static_cast<siq::bf16*>(y);
+  a.part = static_cast<float*>(ws);
+  a.batch = batch;
+  a.side = side;
+  a.dv = vision_dim;
+  a.n = out_features;
+  a.r = factor;
+  const hipError_t e = siq::proj_fwd(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "projector forward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int siq_proj_bwd(const void* x, const void* weight, const void* dy, void* dx, void* dweight, int64_t batch,
+                 int64_t side, int64_t vision_dim, int factor, int64_t out_features, void* ws, size_t ws_bytes,
+                 void* stream) {
+  int rc = check_proj(batch, side, vision_dim, factor, out_features);
+  if (rc) return rc;
+  if (weight == nullptr || !aligned16(weight)) return fail(SIQ_ERR_ALIGNMENT, "weight must be non-NULL and 16-byte aligned");
+  if (dweight != nullptr && !aligned16(dweight)) return fail(SIQ_ERR_ALIGNMENT, "dweight not 16-byte aligned");
+  if (batch > 0) {
+    if (x == nullptr || dy == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "x and dy must not be NULL");
+    if (!aligned16(x) || !aligned16(dy) || (dx != nullptr && !aligned16(dx)))
+      return fail(SIQ_ERR_ALIGNMENT, "x / dy / dx not 16-byte aligned");
+    const size_t need = siq::proj_workspace_bytes(batch, side, vision_dim, factor, out_features);
+    if (dweight != nullptr && need > 0 && (ws == nullptr || ws_bytes < need || !aligned16(ws)))
+      return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
+  }
+  siq::ProjArgs a{};
+  a.x = static_cast<const siq::bf16*>(x);
+  a.weight = static_cast<const siq::bf16*>(weight);
+  a.dy = static_cast<const siq::bf16*>(dy);
+  a.dx = batch > 0 ? static_cast<siq::bf16*>(dx) : nullptr;
+  a.dweight = static_cast<siq::bf16*>(dweight);
+  a.part = static_cast<float*>(ws);
+  a.batch = batch;
+  a.side = side;
+  a.dv = vision_dim;
+  a.n = out_features;
+  a.r = factor;
+  const hipError_t e = siq::proj_bwd(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "projector backward launch failed: %s", hipGetErrorString(e));
+  return ok();
 }
 
 int siq_scale_bf16_inplace(void* data, int64_t numel, const float* scalar, void* stream) {
