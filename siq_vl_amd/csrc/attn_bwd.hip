@@ -173,7 +173,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
     const StepLoad nl = describe(step + 1, buf ^ 1);
 
     const int wq0 = q0 + 32 * g;  // first q row of this wave
-    const bool active = 32 * g < qvalid && (!CAUSAL || wq0 + 31 + off >= kb);
+    // kv quarters past the sequence end have nothing to accumulate
+    const bool active = 32 * g < qvalid && kb < si.k_len && (!CAUSAL || wq0 + 31 + off >= kb);
     if (!active && pf) {
 #pragma unroll
       for (int k = 0; k < StTile::PERW; ++k) issue_k(nl, k);
@@ -470,7 +471,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
     const int kw = kb * BN + 32 * kh;  // first kv row of this half
-    const bool active = kw < si.k_len && (!CAUSAL || kw <= wq0 + 31 + off);
+    const bool active = wq0 < si.q_len && kw < si.k_len && (!CAUSAL || kw <= wq0 + 31 + off);
     if (!active && pf) {
 #pragma unroll
       for (int k = 0; k < Tile::PERW; ++k) issue_k(kh * Tile::PERW + k);

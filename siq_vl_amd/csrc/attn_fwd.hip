@@ -106,7 +106,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
       kt.template issue<true>(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN, nx, wu);
       vt.template issue<true>(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN, nx + TE, wu);
     }
-    const bool active = !CAUSAL || (k0 <= wq_last + off);
+    // a wave whose 32 q rows all lie past the sequence end (the tail of the
+    // last q-tile) has nothing to compute; it still stages its loads
+    const bool active = q0 + 32 * w < si.q_len && (!CAUSAL || (k0 <= wq_last + off));
     if (active) {
       // independent accumulators innermost, so consecutive MFMAs never wait on each other
       f32x16 s[BN / 32];
