@@ -33,6 +33,7 @@ from siq_vl_amd import attention as A
 from siq_vl_amd import cross_entropy as C
 from siq_vl_amd import projector as PJ
 from siq_vl_amd import rope as R
+from siq_vl_amd import splice as SP
 from siq_vl_amd import workloads as W
 
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CUs x 2.4 GHz)
@@ -241,6 +242,62 @@ def bench_projector(steps: int, warmup: int) -> dict:
             "fwd_tflops": fl_f / (fwd_ms * 1e-3) / 1e12, "bwd_tflops": fl_b / (bwd_ms * 1e-3) / 1e12}
 
 
+def bench_splice(steps: int, warmup: int) -> dict:
+    """Vision-token splice forward at config-4 scale: 16384 tokens of Qwen2.5-1.5B (1536
+    features, 151936-row table) of which 4096 are image tokens (16 tiles x 256); the
+    reference's torch ops (embedding, nonzero, index assignment) beside it."""
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(W.SEED)
+    n, hidden, vocab, nimg, img = 16384, 1536, 151936, 4096, 151655
+    ids = torch.randint(0, vocab, (1, n), generator=g)
+    ids[ids == img] = 0
+    ids[0, torch.randperm(n, generator=g)[:nimg]] = img
+    ids = ids.to(dev)
+    weight = (0.02 * torch.randn(vocab, hidden, generator=g)).to(torch.bfloat16).to(dev)
+    vis = torch.randn(nimg, hidden, generator=g).to(torch.bfloat16).to(dev)
+    emb = torch.nn.Embedding(vocab, hidden).to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        emb.weight.copy_(weight)
+    stream = torch.cuda.current_stream(dev)
+    flat = ids.view(-1)
+
+    def timed(fn, reps):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ev = _events(steps + 1)
+        ev[0].record(stream)
+        for i in range(steps):
+            fn()
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+        return per[len(per) // 2] / reps
+
+    def graphed(fn, reps=10):
+        fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(reps):
+                fn()
+        return timed(gr.replay, reps)
+
+    # the kernels alone (the op adds one device-to-host read of the count, as the reference's nonzero does)
+    fwd_ms = graphed(lambda: SP.splice_fwd(flat, weight, vis, img))
+
+    def ref_step():
+        te = emb(ids)
+        positions = (ids == img).nonzero(as_tuple=True)
+        te[positions] = vis
+
+    ref_ms = timed(ref_step, 1)
+    op_ms = timed(lambda: SP.splice_vision_tokens(ids, weight, vis, img), 1)
+    nbytes = SP.splice_bytes(n, hidden)
+    return {"fwd_ms": fwd_ms, "op_ms": op_ms, "ref_ms": ref_ms, "bytes": nbytes,
+            "gbs": nbytes / (fwd_ms * 1e-3) / 1e9}
+
+
 def bench_ce(steps: int, warmup: int, chunk: int) -> dict:
     cfg = W.CONFIG4
     dev = torch.device("cuda")
@@ -340,6 +397,7 @@ def main() -> int:
     ap.add_argument("--skip-ce", action="store_true")
     ap.add_argument("--skip-rope", action="store_true")
     ap.add_argument("--skip-projector", action="store_true")
+    ap.add_argument("--skip-splice", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (3 times): the known-size reference that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -382,6 +440,12 @@ def main() -> int:
         print(f"[bench] projector fwd {proj['fwd_ms'] * 1e3:.1f} us ({proj['fwd_tflops']:.0f} TFLOP/s), bwd "
               f"{proj['bwd_ms'] * 1e3:.1f} us ({proj['bwd_tflops']:.0f} TFLOP/s); reference torch ops fwd+bwd "
               f"{proj['ref_ms'] * 1e3:.1f} us", file=sys.stderr, flush=True)
+    spl = None
+    if not args.skip_splice:
+        spl = bench_splice(max(10, args.steps), args.warmup)
+        print(f"[bench] splice kernels {spl['fwd_ms'] * 1e3:.1f} us ({spl['gbs']:.0f} GB/s), whole op with its count "
+              f"check {spl['op_ms'] * 1e3:.1f} us; reference torch ops {spl['ref_ms'] * 1e3:.1f} us",
+              file=sys.stderr, flush=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
 
     cfg = att["cfg"]
@@ -439,6 +503,15 @@ def main() -> int:
             "roofline": {"bound": "mfma", "achieved": round(proj["tflops"], 1), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(proj["tflops"] / PEAK_BF16_TFLOPS, 4)},
             "reference_torch_ops_fwd_bwd_us": round(proj["ref_ms"] * 1e3, 2)}
+    if spl is not None:
+        line["splice"] = {
+            "workload": "vision-token splice: 16384 tokens x 1536 (4096 image tokens), 151936-row embedding table",
+            "kernels_us": round(spl["fwd_ms"] * 1e3, 2),
+            "timing": "10 launches captured in a HIP graph, replayed; events on the launch stream",
+            "roofline": {"bound": "hbm", "achieved": round(spl["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(spl["gbs"] / PEAK_HBM_GBS, 4), "algorithmic_bytes": spl["bytes"]},
+            "op_with_count_check_us": round(spl["op_ms"] * 1e3, 2),
+            "reference_torch_ops_us": round(spl["ref_ms"] * 1e3, 2)}
     if cpu:
         line["host"] = cpu["host"]
     print(json.dumps(line), flush=True)

@@ -1,7 +1,7 @@
 /*
  * siq_kernels.h -- C ABI of the SiQ-VL training hot path on MI355X (gfx950).
  *
- * Four operators, all hand-written HIP behind this plain-C boundary:
+ * Five operators, all hand-written HIP behind this plain-C boundary:
  *   1. varlen (cu_seqlens-packed) flash attention, forward and backward,
  *      causal GQA (Qwen2.5 decoder) or bidirectional (SigLIP tower);
  *   2. fused lm_head linear + cross-entropy, forward and backward, without
@@ -9,7 +9,9 @@
  *   3. the rotary position embedding of q and k that precedes attention in
  *      the decoder, forward and backward, in one pass each;
  *   4. the pixel-shuffle projector (vision features to text embeddings),
- *      forward and backward, with the shuffle folded into the GEMM loads.
+ *      forward and backward, with the shuffle folded into the GEMM loads;
+ *   5. the splice of the projected vision rows into the token embeddings,
+ *      fused with the embedding gather.
  *
  * Conventions
  *  - Every entry point returns an int status (SIQ_OK = 0, < 0 on error) and
@@ -186,6 +188,36 @@ int siq_proj_fwd(const void* x, const void* weight, void* y, int64_t batch, int6
 int siq_proj_bwd(const void* x, const void* weight, const void* dy, void* dx, void* dweight, int64_t batch,
                  int64_t side, int64_t vision_dim, int factor, int64_t out_features, void* workspace,
                  size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Vision-token splice fused with the embedding gather.
+ *
+ * Replaces, in SiQ_VLForCausalLM.forward (siq_vl/model/modeling.py:252-270),
+ * the embedding lookup of input_ids (:253), the nonzero() of the image-token
+ * positions (:257), their count check (:259-267) and the index assignment of
+ * the flattened vision rows (:269-270):
+ *   out[p] = vision[r]          if input_ids[p] == image_token_id, r = number
+ *                               of image tokens before p (row-major order);
+ *   out[p] = weight[input_ids[p]] otherwise.
+ * input_ids [n_tokens] int64; weight [vocab, hidden], vision [n_vision,
+ * hidden], out [n_tokens, hidden]: bf16, contiguous, 16-byte aligned;
+ * hidden % 8 == 0.  Outputs (device): image_pos [n_vision] int32 = token index
+ * of vision row r; counts[0] = image tokens found (the caller raises the
+ * reference's ValueError when it differs from n_vision: rows of image tokens
+ * beyond n_vision are written as zeros), counts[1] = ids outside [0, vocab)
+ * (written as zeros; the reference's embedding would raise).  Workspace:
+ * siq_splice_workspace_bytes(n_tokens).
+ *
+ * siq_gather_rows: dst[i] = src[rows[i]], i < n (rows of hidden bf16): the
+ * backward's vision-row gradient (IndexPutBackward of :270) from image_pos.
+ * ------------------------------------------------------------------------- */
+size_t siq_splice_workspace_bytes(int64_t n_tokens);
+
+int siq_splice_fwd(const int64_t* input_ids, int64_t n_tokens, const void* weight, int64_t vocab, int64_t hidden,
+                   const void* vision, int64_t n_vision, int64_t image_token_id, void* out, int32_t* image_pos,
+                   int64_t* counts, void* workspace, size_t workspace_bytes, void* stream);
+
+int siq_gather_rows(const void* src, const int32_t* rows, int64_t n, int64_t hidden, void* dst, void* stream);
 
 #ifdef __cplusplus
 }

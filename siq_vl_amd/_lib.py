@@ -57,6 +57,10 @@ _PROTOS = {
                             _c_void_p]),
     "siq_proj_bwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _i64,
                             _c_void_p, _size, _c_void_p]),
+    "siq_splice_workspace_bytes": (_size, [_i64]),
+    "siq_splice_fwd": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
+                              _c_void_p, _c_void_p, _size, _c_void_p]),
+    "siq_gather_rows": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
     "siq_rope_fwd": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32, _i32, _i32,

@@ -13,6 +13,7 @@
 #include "flce.h"
 #include "proj.h"
 #include "rope.h"
+#include "splice.h"
 
 namespace {
 
@@ -457,6 +458,57 @@ int siq_proj_bwd(const void* x, const void* weight, const void* dy, void* dx, vo
   a.r = factor;
   const hipError_t e = siq::proj_bwd(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "projector backward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+size_t siq_splice_workspace_bytes(int64_t n_tokens) {
+  if (n_tokens < 0) return 0;
+  return align256(sizeof(int32_t) * (size_t)(n_tokens > 0 ? n_tokens : 1));
+}
+
+int siq_splice_fwd(const int64_t* input_ids, int64_t n_tokens, const void* weight, int64_t vocab, int64_t hidden,
+                   const void* vision, int64_t n_vision, int64_t image_token_id, void* out, int32_t* image_pos,
+                   int64_t* counts, void* ws, size_t ws_bytes, void* stream) {
+  if (n_tokens < 0 || n_vision < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "n_tokens and n_vision must be >= 0");
+  if (n_tokens >= (int64_t(1) << 31) || n_vision >= (int64_t(1) << 31))
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "n_tokens and n_vision must be < 2^31");
+  if (vocab <= 0 || hidden <= 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "vocab and hidden must be positive");
+  if (hidden % 8 != 0) return fail(SIQ_ERR_UNSUPPORTED, "hidden (%lld) must be a multiple of 8", (long long)hidden);
+  if (counts == nullptr || (reinterpret_cast<uintptr_t>(counts) & 7u))
+    return fail(SIQ_ERR_ALIGNMENT, "counts must be a non-NULL 8-byte aligned int64[2]");
+  if (weight == nullptr || !aligned16(weight)) return fail(SIQ_ERR_ALIGNMENT, "weight must be non-NULL and 16-byte aligned");
+  if (n_vision > 0 && (vision == nullptr || !aligned16(vision) || image_pos == nullptr))
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "vision (16-byte aligned) and image_pos must not be NULL");
+  if (n_tokens > 0 && (input_ids == nullptr || out == nullptr || !aligned16(out)))
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "input_ids and out (16-byte aligned) must not be NULL");
+  const size_t need = siq_splice_workspace_bytes(n_tokens);
+  if (ws == nullptr || ws_bytes < need || !aligned16(ws))
+    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
+  siq::SpliceArgs a{};
+  a.ids = input_ids;
+  a.weight = static_cast<const siq::bf16*>(weight);
+  a.vision = static_cast<const siq::bf16*>(vision);
+  a.out = static_cast<siq::bf16*>(out);
+  a.rank = static_cast<int32_t*>(ws);
+  a.n = n_tokens;
+  a.vocab = vocab;
+  a.hidden = hidden;
+  a.n_vision = n_vision;
+  a.image_id = image_token_id;
+  const hipError_t e = siq::splice_fwd(a, image_pos, counts, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "splice launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int siq_gather_rows(const void* src, const int32_t* rows, int64_t n, int64_t hidden, void* dst, void* stream) {
+  if (n < 0 || n >= (int64_t(1) << 31)) return fail(SIQ_ERR_INVALID_ARGUMENT, "n must be in [0, 2^31)");
+  if (hidden <= 0 || hidden % 8 != 0) return fail(SIQ_ERR_UNSUPPORTED, "hidden (%lld) must be a positive multiple of 8", (long long)hidden);
+  if (n == 0) return ok();
+  if (src == nullptr || rows == nullptr || dst == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "src, rows and dst must not be NULL");
+  if (!aligned16(src) || !aligned16(dst)) return fail(SIQ_ERR_ALIGNMENT, "src / dst not 16-byte aligned");
+  const hipError_t e = siq::gather_rows(static_cast<const siq::bf16*>(src), rows, n, hidden, static_cast<siq::bf16*>(dst),
+                                        static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "gather launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 
