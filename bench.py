@@ -469,7 +469,7 @@ def main() -> int:
                    "pct_bf16_peak": round(100.0 * att["tflops"] / PEAK_BF16_TFLOPS, 2),
                    "fwd_ms": round(att["fwd_ms"], 4), "bwd_ms": round(att["bwd_ms"], 4),
                    "fwd_tflops": round(att["fwd_tflops"], 2), "bwd_tflops": round(att["bwd_tflops"], 2)},
-        "roofline": {"bound": "mfma", "kernel": "attention backward call (preprocess + dK/dV + dQ kernels)",
+        "roofline": {"bound": "mfma", "kernel": "attention backward call (schedule + dQ + dK/dV + split-tile sum kernels)",
                      "achieved": round(bwd_achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(bwd_achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": measured_traffic("attention_bwd_config2"),
