@@ -8,7 +8,14 @@
 //   dZ   = (softmax(z_n) - onehot(y_n)) * inv_den  (0 for ignored rows),
 //   dH = dZ W,  dW = dZ^T H.
 //
-// Pipeline per chunk of C token rows (the only logits-sized buffer is one
+// Rows whose label is ignore_index (or out of range) contribute nothing: their
+// dH row is zero and they add nothing to the loss or dW.  So the valid rows
+// are first compacted, in order, into a contiguous buffer (padded with zero
+// rows to the next 256-row tile), every stage below runs on the compacted rows
+// only (each workgroup reads the valid count on the device and returns early
+// past it), and dH rows are scattered back to their positions.
+//
+// Pipeline per chunk of C compacted rows (the only logits-sized buffer is one
 // chunk's softmax numerators):
 //  1. logits GEMM  Z^T = W H_c^T (MFMA, 256x256 tiles, K = hdim).  The epilogue
 //     never writes z: per (token, 256-column vocab tile) it keeps the tile
@@ -42,7 +49,8 @@ struct LogitsArgs {
   float* mpart;           // [nc, nvt] tile max (log2 units)
   float* spart;           // [nc, nvt] tile sum of exp2(z2 - m)
   float* zy;              // [nc] label logit (natural units)
-  int64_t V, nc, nvt;
+  const int64_t* nvalid;  // valid (compacted) rows in all chunks
+  int64_t V, nc, nvt, c0;
   int nI, nJ;
 };
 
@@ -51,6 +59,7 @@ __global__ __launch_bounds__(NT) void flce_logits_kernel(const LogitsArgs p) {
   int ti, tj;
   if (!tile_of(p.nI, p.nJ, 4, ti, tj)) return;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
+  if (j0 >= *p.nvalid - p.c0) return;  // token tile holds no valid row
   f32x16 acc[4][2];
   gemm_core<true, true>(smem, p.W, p.H, i0, j0, 0, p.W.cols, acc);
 
@@ -150,7 +159,8 @@ struct RowArgs {
   bf16* E;               // [nc, V]: E on entry, dZ on exit
   float* loss_row;       // [nc] (chunk slice)
   const float* invden;
-  int64_t nc, nvt, V, ignore_index;
+  const int64_t* nvalid;
+  int64_t nc, nvt, V, ignore_index, c0;
 };
 
 // One wave per token row.  lse2 = M + log2(sum_t s_t 2^(m_t - M)); then the
@@ -159,7 +169,8 @@ struct RowArgs {
 __global__ __launch_bounds__(256) void flce_row_kernel(const RowArgs p) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= p.nc) return;
+  // rows past the last token tile with a valid row are read by no GEMM
+  if (row >= p.nc || row >= ((*p.nvalid - p.c0 + BJ - 1) / BJ) * BJ) return;
   const float* m = p.mpart + row * p.nvt;
   const float* s = p.spart + row * p.nvt;
   float mx = -INFINITY;
@@ -184,32 +195,37 @@ __global__ __launch_bounds__(256) void flce_row_kernel(const RowArgs p) {
     for (int64_t c = lane; c < nchunk; c += 64) st_bf16x8(e + 8 * c, zero_bf16x8());
     return;
   }
-  // U chunks per lane in flight: one 16-byte load at a time leaves the pass latency-bound
+  // U chunks per lane in flight, with their tile maxima: chunk c (columns 8 c ..
+  // 8 c + 7) lies in tile c / 32, so lane chunks c0 + 64 u sit in tiles
+  // c0 / 32 + 2 u, and all 2 U loads of a batch go out before the first use
+  // (a per-chunk load of m would wait once per chunk)
   constexpr int U = 8;
-  for (int64_t c0 = lane; c0 < nchunk; c0 += 64 * U) {
+  auto chunk = [&](const bf16x8& x, float mt, int64_t c) {
+    const int64_t v0 = 8 * c;
+    const float fv = exp2f_fast(mt - lse2) * gv;
+    bf16x8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (bf16)((float)x[i] * fv);
+    const int64_t yrel = yv - v0;
+    if (yrel >= 0 && yrel < 8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = (i == yrel) ? (bf16)((float)x[i] * fv - gv) : o[i];
+    }
+    st_bf16x8(e + v0, o);
+  };
+  int64_t c0 = lane;
+  for (; c0 + 64 * (U - 1) < nchunk; c0 += 64 * U) {
     bf16x8 x[U];
+    float mt[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t c = c0 + 64 * u;
-      x[u] = c < nchunk ? ld_bf16x8(e + 8 * c) : zero_bf16x8();
+      x[u] = ld_bf16x8(e + 8 * (c0 + 64 * u));
+      mt[u] = m[(c0 >> 5) + 2 * u];
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t c = c0 + 64 * u;
-      if (c >= nchunk) break;
-      const int64_t v0 = 8 * c;
-      const float fv = exp2f_fast(m[v0 / kVT] - lse2) * gv;
-      bf16x8 o;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (bf16)((float)x[u][i] * fv);
-      const int64_t yrel = yv - v0;
-      if (yrel >= 0 && yrel < 8) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = (i == yrel) ? (bf16)((float)x[u][i] * fv - gv) : o[i];
-      }
-      st_bf16x8(e + v0, o);
-    }
+    for (int u = 0; u < U; ++u) chunk(x[u], mt[u], c0 + 64 * u);
   }
+  for (; c0 < nchunk; c0 += 64) chunk(ld_bf16x8(e + 8 * c0), m[c0 >> 5], c0);
 }
 
 // ---------------------------------------------------------------- dH
@@ -218,7 +234,9 @@ struct DhArgs {
   GOp E;         // dZ [nc, V] read as B[j = tok][k = v]
   bf16* dh;      // dhidden rows of the chunk [nc, hdim] (used when splits == 1)
   float* part;   // [splits, nc, hdim]
-  int64_t hdim, nc, kper;
+  const int32_t* rows;    // compacted row -> original row (whole batch)
+  const int64_t* nvalid;
+  int64_t hdim, nc, kper, c0;
   int nI, nJ, splits;
 };
 
@@ -228,6 +246,8 @@ __global__ __launch_bounds__(NT) void flce_dh_kernel(const DhArgs p) {
   if (!tile_of(p.nI, p.nJ, p.nI, ti, tj)) return;
   const int split = blockIdx.y;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
+  const int64_t nv = *p.nvalid - p.c0;
+  if (j0 >= nv) return;
   const int64_t kb = split * p.kper;
   const int64_t ke = min(p.E.cols, kb + p.kper);
   f32x16 acc[4][2];
@@ -238,6 +258,8 @@ __global__ __launch_bounds__(NT) void flce_dh_kernel(const DhArgs p) {
   for (int b = 0; b < 2; ++b) {
     const int64_t tok = j0 + 64 * wj + 32 * b + l32;
     if (tok >= p.nc) continue;
+    if (p.splits == 1 && tok >= nv) continue;  // padding row
+    const int64_t orow = p.splits == 1 ? p.rows[p.c0 + tok] : 0;
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -248,7 +270,7 @@ __global__ __launch_bounds__(NT) void flce_dh_kernel(const DhArgs p) {
           bf16x8 o;
 #pragma unroll
           for (int i = 0; i < 8; ++i) o[i] = (bf16)acc[a][b][8 * jj + i];
-          st_bf16x8(p.dh + tok * p.hdim + hh, o);
+          st_bf16x8(p.dh + orow * p.hdim + hh, o);
         } else {
           float* dst = p.part + ((int64_t)split * p.nc + tok) * p.hdim + hh;
           f32x4 lo, hi;
@@ -264,10 +286,16 @@ __global__ __launch_bounds__(NT) void flce_dh_kernel(const DhArgs p) {
   }
 }
 
+// dH rows of the chunk: the splits' fp32 partial sums added in split order,
+// each compacted row written to its original row.
 __global__ __launch_bounds__(256) void flce_dh_sum_kernel(const float* __restrict__ part, bf16* __restrict__ dh,
-                                                          int64_t nvec, int64_t stride, int splits) {
-  // nvec groups of 8 elements; part is [splits][stride] with stride = nc * hdim.
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += (int64_t)gridDim.x * 256) {
+                                                          const int32_t* __restrict__ rows,
+                                                          const int64_t* __restrict__ nvalid, int64_t c0, int64_t nc,
+                                                          int64_t hdim, int splits) {
+  // part is [splits][nc * hdim]; groups of 8 elements, hdim / 8 per row
+  const int64_t nv = min(nc, *nvalid - c0);
+  const int64_t gpr = hdim / 8, stride = nc * hdim;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nv * gpr; i += (int64_t)gridDim.x * 256) {
     f32x4 a = *reinterpret_cast<const f32x4*>(part + 8 * i);
     f32x4 b = *reinterpret_cast<const f32x4*>(part + 8 * i + 4);
     for (int s = 1; s < splits; ++s) {
@@ -280,7 +308,8 @@ __global__ __launch_bounds__(256) void flce_dh_sum_kernel(const float* __restric
       o[k] = (bf16)a[k];
       o[4 + k] = (bf16)b[k];
     }
-    st_bf16x8(dh + 8 * i, o);
+    const int64_t r = i / gpr;
+    st_bf16x8(dh + (int64_t)rows[c0 + r] * hdim + 8 * (i - r * gpr), o);
   }
 }
 
@@ -290,7 +319,8 @@ struct DwArgs {
   GOp Et;        // dZ [nc, V] read as B[j = v][k = tok]
   bf16* dw;      // [V, hdim]
   float* acc32;  // [V, hdim] fp32 accumulator across chunks
-  int64_t hdim, V;
+  const int64_t* nvalid;
+  int64_t hdim, V, c0;
   int nI, nJ;
   int mode;      // 0: bf16 store; 1: fp32 store; 2: fp32 add; 3: fp32 add + bf16 store
 };
@@ -300,8 +330,12 @@ __global__ __launch_bounds__(NT) void flce_dw_kernel(const DwArgs p) {
   int ti, tj;
   if (!tile_of(p.nI, p.nJ, p.nI, ti, tj)) return;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
+  // tokens past the last 64-row step with a valid row are skipped (those up to
+  // it are zero padding)
+  const int64_t nv = *p.nvalid - p.c0;
+  const int64_t ke = min(p.Ht.rows, nv > 0 ? ((nv + BK - 1) / BK) * BK : (int64_t)0);
   f32x16 acc[4][2];
-  gemm_core<false, false>(smem, p.Ht, p.Et, i0, j0, 0, p.Ht.rows, acc);
+  gemm_core<false, false>(smem, p.Ht, p.Et, i0, j0, 0, ke, acc);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int wi = w & 1, wj = w >> 1;
 #pragma unroll
@@ -371,11 +405,94 @@ __global__ __launch_bounds__(1024) void flce_count_kernel(const int64_t* __restr
   }
 }
 
+// Valid rows in order, compacted: rows[k] = the k-th row whose label counts,
+// *nvalid = their number.  One workgroup; per round 16 chunks of 1024 labels
+// are loaded at once, each wave ballots its valid lanes, and one prefix over
+// the 256 (chunk, wave) counts places every valid row.
+__global__ __launch_bounds__(1024) void flce_compact_kernel(const int64_t* __restrict__ y, int64_t n, int64_t V,
+                                                            int64_t ignore_index, int32_t* __restrict__ rows,
+                                                            int64_t* __restrict__ nvalid) {
+  constexpr int CT = 1024, NWV = CT / 64, PER = 16;
+  static_assert(PER * NWV == 256, "one (chunk, wave) count per lane quarter");
+  __shared__ int cnt_sh[PER * NWV];  // valid rows of (chunk i, wave w) at i * NWV + w, in row order
+  __shared__ long long carry_sh;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;  // lanes before this one
+  if (tid == 0) carry_sh = 0;
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < n; c0 += (int64_t)CT * PER) {
+    int64_t v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int64_t r = c0 + (int64_t)i * CT + tid;
+      v[i] = r < n ? y[r] : ignore_index;
+    }
+    uint64_t m[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      m[i] = __ballot(v[i] != ignore_index && v[i] >= 0 && v[i] < V);
+      if (lane == 0) cnt_sh[i * NWV + wv] = __popcll(m[i]);
+    }
+    __syncthreads();
+    // exclusive prefix of the 256 counts in row order: lane l holds entries 4 l .. 4 l + 3
+    const int a0 = cnt_sh[4 * lane], a1 = cnt_sh[4 * lane + 1], a2 = cnt_sh[4 * lane + 2], a3 = cnt_sh[4 * lane + 3];
+    const int lsum = a0 + a1 + a2 + a3;
+    int incl = lsum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o);
+      if (lane >= o) incl += t;
+    }
+    const int total = __shfl(incl, 63);
+    // entry i * NWV + wv sits in lane 4 i + wv / 4 at position wv % 4 (the same position for every i)
+    const int k = wv & 3;
+    const int mine = incl - lsum + (k > 0 ? a0 : 0) + (k > 1 ? a1 : 0) + (k > 2 ? a2 : 0);
+    const long long carry = carry_sh;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const long long r = carry + __shfl(mine, 4 * i + (wv >> 2)) + __popcll(m[i] & below);
+      if ((m[i] >> lane) & 1) rows[r] = (int32_t)(c0 + (int64_t)i * CT + tid);
+    }
+    __syncthreads();
+    if (tid == 0) carry_sh += total;
+    __syncthreads();
+  }
+  if (tid == 0) *nvalid = carry_sh;
+}
+
+// The compacted operands: Hc[k] = H[rows[k]], yc[k] = y[rows[k]] for k < nvalid,
+// zero rows and ignore_index up to the next multiple of 256 (the padding the
+// GEMM tiles read); and dH = 0 on every row whose label does not count.  One
+// wave per row, 16 bytes per lane per step.
+__global__ __launch_bounds__(256) void flce_gather_kernel(const bf16* __restrict__ H, const int64_t* __restrict__ y,
+                                                          const int32_t* __restrict__ rows,
+                                                          const int64_t* __restrict__ nvalid, int64_t n, int64_t hdim,
+                                                          int64_t V, int64_t ignore_index, bf16* __restrict__ Hc,
+                                                          int64_t* __restrict__ yc, bf16* __restrict__ dh) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nvec = hdim / 8, nv = *nvalid, npad = ((nv + 255) / 256) * 256;
+  const int64_t wstep = (int64_t)gridDim.x * 4;
+  for (int64_t k = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); k < npad; k += wstep) {
+    const bool real = k < nv;
+    const int64_t src = real ? rows[k] : 0;
+    if (lane == 0) yc[k] = real ? y[src] : ignore_index;
+    for (int64_t c = lane; c < nvec; c += 64)
+      st_bf16x8(Hc + k * hdim + 8 * c, real ? ld_bf16x8(H + src * hdim + 8 * c) : zero_bf16x8());
+  }
+  for (int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < n; t += wstep) {
+    const int64_t v = y[t];
+    if (v != ignore_index && v >= 0 && v < V) continue;
+    for (int64_t c = lane; c < nvec; c += 64) st_bf16x8(dh + t * hdim + 8 * c, zero_bf16x8());
+  }
+}
+
 __global__ __launch_bounds__(1024) void flce_loss_kernel(const float* __restrict__ loss_row, int64_t n,
+                                                         const int64_t* __restrict__ nvalid,
                                                          const float* __restrict__ invden, float* loss) {
   __shared__ float sm[1024];
   float acc = 0.f;
-  for (int64_t i = threadIdx.x; i < n; i += 1024) acc += loss_row[i];
+  const int64_t nv = min(n, *nvalid);
+  for (int64_t i = threadIdx.x; i < nv; i += 1024) acc += loss_row[i];
   sm[threadIdx.x] = acc;
   __syncthreads();
   for (int s = 512; s >= 1; s >>= 1) {
@@ -408,7 +525,7 @@ __global__ __launch_bounds__(256) void zero_bf16_kernel(bf16* __restrict__ x, in
 
 // ---------------------------------------------------------------- workspace
 struct Layout {
-  size_t invden, loss_row, mpart, spart, zy, E, part, acc32, total;
+  size_t invden, loss_row, mpart, spart, zy, E, part, acc32, rows, hc, yc, total;
   int64_t chunk, nvt, splits;
 };
 
@@ -445,6 +562,13 @@ Layout layout(int64_t n, int64_t hdim, int64_t V, int64_t chunk, bool need_dw) {
   if (L.splits > 1) off += al(sizeof(float) * (size_t)(L.splits * L.chunk * hdim));
   L.acc32 = off;
   if (need_dw && nchunks > 1) off += al(sizeof(float) * (size_t)(V * hdim));
+  const int64_t npad = ((n > 0 ? n : 1) + 255) / 256 * 256;
+  L.rows = off;
+  off += al(sizeof(int32_t) * (size_t)npad);
+  L.hc = off;
+  off += al(sizeof(bf16) * (size_t)(npad * hdim));
+  L.yc = off;
+  off += al(sizeof(int64_t) * (size_t)npad);
   L.total = off;
   return L;
 }
@@ -467,16 +591,30 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
   bf16* E = reinterpret_cast<bf16*>(ws + L.E);
   float* part = reinterpret_cast<float*>(ws + L.part);
   float* acc32 = reinterpret_cast<float*>(ws + L.acc32);
+  int64_t* nvalid = reinterpret_cast<int64_t*>(ws + L.invden) + 1;
+  int32_t* rows = reinterpret_cast<int32_t*>(ws + L.rows);
+  bf16* hcomp = reinterpret_cast<bf16*>(ws + L.hc);
+  int64_t* ycomp = reinterpret_cast<int64_t*>(ws + L.yc);
   const int64_t V = a.vocab, Hd = a.hdim;
 
   hipLaunchKernelGGL(flce_count_kernel, dim3(1), dim3(1024), 0, stream, a.labels, a.n, V, a.ignore_index,
                      a.reduction, a.divisor, a.count, a.bad_labels, invden);
+  hipLaunchKernelGGL(flce_compact_kernel, dim3(1), dim3(1024), 0, stream, a.labels, a.n, V, a.ignore_index, rows,
+                     nvalid);
+  if (a.n > 0) {
+    int64_t blocks = (a.n + 3) / 4;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(flce_gather_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a.hidden, a.labels, rows,
+                       nvalid, a.n, Hd, V, a.ignore_index, hcomp, ycomp, a.dhidden);
+  }
+  // chunks of compacted rows: the host sizes them for n rows; those past the
+  // valid count return at once
   const int64_t nchunks = a.n > 0 ? (a.n + L.chunk - 1) / L.chunk : 0;
   for (int64_t ci = 0; ci < nchunks; ++ci) {
     const int64_t c0 = ci * L.chunk;
     const int64_t nc = (a.n - c0) < L.chunk ? (a.n - c0) : L.chunk;
-    const bf16* Hc = a.hidden + c0 * Hd;
-    const int64_t* yc = a.labels + c0;
+    const bf16* Hc = hcomp + c0 * Hd;
+    const int64_t* yc = ycomp + c0;
 
     LogitsArgs lg{};
     lg.W = GOp{a.weight, Hd, V, Hd};
@@ -486,6 +624,8 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
     lg.mpart = mpart;
     lg.spart = spart;
     lg.zy = zy;
+    lg.nvalid = nvalid;
+    lg.c0 = c0;
     lg.V = V;
     lg.nc = nc;
     lg.nvt = L.nvt;
@@ -505,6 +645,8 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
     rw.E = E;
     rw.loss_row = loss_row + c0;
     rw.invden = invden;
+    rw.nvalid = nvalid;
+    rw.c0 = c0;
     rw.nc = nc;
     rw.nvt = L.nvt;
     rw.V = V;
@@ -514,8 +656,11 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
     DhArgs dh{};
     dh.Wt = GOp{a.weight, Hd, V, Hd};
     dh.E = GOp{E, V, nc, V};
-    dh.dh = a.dhidden + c0 * Hd;
+    dh.dh = a.dhidden;
     dh.part = part;
+    dh.rows = rows;
+    dh.nvalid = nvalid;
+    dh.c0 = c0;
     dh.hdim = Hd;
     dh.nc = nc;
     dh.splits = (int)L.splits;
@@ -534,8 +679,8 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
       const int64_t nvec = nc * Hd / 8;
       int64_t blocks = (nvec + 255) / 256;
       if (blocks > 4096) blocks = 4096;
-      hipLaunchKernelGGL(flce_dh_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, part,
-                         a.dhidden + c0 * Hd, nvec, nc * Hd, (int)L.splits);
+      hipLaunchKernelGGL(flce_dh_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, part, a.dhidden, rows,
+                         nvalid, c0, nc, Hd, (int)L.splits);
     }
 
     if (a.dweight != nullptr) {
@@ -544,6 +689,8 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
       dw.Et = GOp{E, V, nc, V};
       dw.dw = a.dweight;
       dw.acc32 = acc32;
+      dw.nvalid = nvalid;
+      dw.c0 = c0;
       dw.hdim = Hd;
       dw.V = V;
       dw.nI = (int)((Hd + BI - 1) / BI);
@@ -564,7 +711,7 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
     if (blocks > 4096) blocks = 4096;
     hipLaunchKernelGGL(zero_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a.dweight, nvec);
   }
-  hipLaunchKernelGGL(flce_loss_kernel, dim3(1), dim3(1024), 0, stream, loss_row, a.n, invden, a.loss);
+  hipLaunchKernelGGL(flce_loss_kernel, dim3(1), dim3(1024), 0, stream, loss_row, a.n, nvalid, invden, a.loss);
   return hipGetLastError();
 }
 
