@@ -240,10 +240,23 @@ struct DhArgs {
   int nI, nJ, splits;
 };
 
+// dH tiles: block b runs on XCD x = b % 8, which takes token tiles x, x + 8,
+// ... in turn, each with its nI hdim tiles (consecutive blocks there, sharing
+// the dZ slab through the XCD's L2).  Token tiles past the valid rows are
+// empty, so striding them over the XCDs keeps every XCD equally loaded
+// (a contiguous run per XCD would leave the last XCDs idle).  The grid is
+// 8 nI ceil(nJ / 8) blocks.
+__device__ __forceinline__ bool dh_tile_of(int nI, int nJ, int& ti, int& tj) {
+  const int x = (int)(blockIdx.x % kXcds), k = (int)(blockIdx.x / kXcds);
+  ti = k % nI;
+  tj = x + kXcds * (k / nI);
+  return tj < nJ;
+}
+
 __global__ __launch_bounds__(NT) void flce_dh_kernel(const DhArgs p) {
   __shared__ __align__(16) bf16 smem[4 * SLAB];
   int ti, tj;
-  if (!tile_of(p.nI, p.nJ, p.nI, ti, tj)) return;
+  if (!dh_tile_of(p.nI, p.nJ, ti, tj)) return;
   const int split = blockIdx.y;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
   const int64_t nv = *p.nvalid - p.c0;
@@ -533,7 +546,7 @@ size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
 int dh_splits(int64_t hdim, int64_t chunk) {
   const int64_t tiles = ((hdim + BI - 1) / BI) * ((chunk + BJ - 1) / BJ);
-  int64_t s = (1024 + tiles - 1) / tiles;
+  int64_t s = (2048 + tiles - 1) / tiles;
   if (s < 1) s = 1;
   if (s > 8) s = 8;
   return (int)s;
@@ -671,8 +684,7 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
     dh.nI = (int)((Hd + BI - 1) / BI);
     dh.nJ = (int)((nc + BJ - 1) / BJ);
     {
-      const int total = dh.nI * dh.nJ;
-      const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
+      const int grid = kXcds * dh.nI * ((dh.nJ + kXcds - 1) / kXcds);
       hipLaunchKernelGGL(flce_dh_kernel, dim3(grid, (unsigned)L.splits), dim3(NT), 0, stream, dh);
     }
     if (L.splits > 1) {
