@@ -75,6 +75,36 @@ def test_all_ignored_gives_nan_and_zero_grads():
     assert np.all(dh == 0.0) and np.all(dw == 0.0)
 
 
+def test_no_ignored_rows_several_chunks():
+    h, w, y = make(600, 256, 1000, seed=8, ignore_frac=0.0)
+    loss, count, bad, dh, dw = run(h, w, y, 256)
+    ref = oc.linear_ce(h, w, y)
+    assert count == ref["count"] == 600 and bad == 0
+    assert abs(loss - ref["loss"]) <= TOL * abs(ref["loss"])
+    assert rel(dh, ref["dh"]) <= TOL and rel(dw, ref["dw"]) <= TOL
+
+
+@pytest.mark.parametrize("chunk", [4096, 512])
+def test_ignored_rows_cost_nothing_but_a_zero_row(chunk):
+    """Rows whose label is ignored are compacted away before the GEMMs: the batch
+    gives bitwise the loss, dW and valid-row dH of the valid rows alone."""
+    g = torch.Generator().manual_seed(9)
+    h = torch.randn(2048, 512, generator=g).to(torch.bfloat16)
+    w = (0.05 * torch.randn(4096, 512, generator=g)).to(torch.bfloat16)
+    y = W.span_masked_labels(2048, 4096, 0.3, g)
+    valid = (y != -100).numpy()
+    print(f"flce compaction chunk={chunk} valid={int(valid.sum())}", flush=True)
+    full = run(h, w, y, chunk)
+    sub = run(h[valid], w, y[valid], chunk)
+    assert full[1] == sub[1] == int(valid.sum())
+    assert full[0] == sub[0]
+    assert np.array_equal(full[3][valid], sub[3]) and np.all(full[3][~valid] == 0.0)
+    if chunk >= 2048:  # one chunk either way: the same rows in the same k-steps
+        assert np.array_equal(full[4], sub[4])
+    else:
+        assert rel(full[4], sub[4]) <= 1e-2
+
+
 def test_qwen_vocab_vs_oracle():
     h, w, y = make(256, 1536, W.QWEN_VOCAB, seed=4, wscale=0.02)
     print("flce qwen vocab n=256", flush=True)
