@@ -152,8 +152,10 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
   }
 
   // dK/dV work items.  1: kv tiles per sequence (prefix sums) and the total
-  // number of steps (per kv-head).
-  int* tfirst = seqbuf;  // [batch + 1] first flattened kv tile of each sequence
+  // number of steps (per kv-head).  The prefix array lives in LDS when it
+  // fits (no global write / read-back between the passes), else in seqbuf.
+  __shared__ int tfirst_sh[kSchedKeys];
+  int* tfirst = batch + 1 <= kSchedKeys ? tfirst_sh : seqbuf;  // [batch + 1] first flattened kv tile of each sequence
   long long mine = 0;
   for (int b = tid; b < batch; b += kSchedThreads) {
     const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
