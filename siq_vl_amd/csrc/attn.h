@@ -19,7 +19,10 @@ constexpr int kSchedKeys = 2048;
 // piece order, by a small kernel after the dK/dV kernel.
 constexpr int kSplitTarget = 256;
 constexpr int kMinSplitSteps = 4;
-constexpr int kSplitSlots = 2 * kSplitTarget + 2;  // bound on sum(pieces x hkv) over split tiles
+// Pieces longer than this many steps amortise their fp32 partial sums, so they
+// are cut twice as fine (piece length >= hkv total / (2 kSplitTarget)).
+constexpr int kLongPiece = 256;
+constexpr int kSplitSlots = 4 * kSplitTarget + 2;  // bound on sum(pieces x hkv) over split tiles
 constexpr int kMaxSplitTiles = kSplitSlots / 2;    // a split tile has >= 2 pieces
 constexpr int kXcds = 8;                           // MI355X: workgroup b runs on XCD b % 8
 
@@ -88,7 +91,9 @@ struct AttnParams {
 // holding `total` tokens: sum ceil(L_b / rows) <= total / rows + batch.
 inline int64_t tile_cap(int64_t total, int batch, int rows) { return total / rows + batch + 1; }
 // Upper bound on the number of dK/dV work items (tiles plus extra pieces).
-inline int64_t kv_item_cap(int64_t total_k, int batch) { return tile_cap(total_k, batch, kBwdBN) + kSplitTarget + 1; }
+inline int64_t kv_item_cap(int64_t total_k, int batch) {
+  return tile_cap(total_k, batch, kBwdBN) + 2 * kSplitTarget + 1;
+}
 
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,
                            int causal, int n_rep, int hkv, SeqInfo* seq, QTile* qtiles, int qrows, int qcap,

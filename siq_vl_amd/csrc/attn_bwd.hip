@@ -317,10 +317,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
 
 // dK / dV of split tiles: the pieces' fp32 sums added in piece order (so the
 // result does not depend on which piece ran when), scaled and written as bf16.
-// One workgroup = ROWS rows of one split tile and kv-head (blockIdx.x = tile *
-// NCH + row chunk); thread x owns float4 column x % COLS of [dK | dV] and
-// rows x / COLS + RSTEP u (u < U) of the chunk, whose loads are in flight
-// together.
+// A work unit = ROWS rows of one split tile and kv-head (unit = tile * NCH +
+// row chunk, kv-head = blockIdx.y); the workgroups stride over the units of
+// the split tiles that exist.  Thread x owns float4 column x % COLS of
+// [dK | dV] and rows x / COLS + RSTEP u (u < U) of the chunk, whose loads are
+// in flight together.
 template <int D>
 struct DkvSum {
   static constexpr int C4 = D / 4, COLS = 2 * C4, RSTEP = 256 / COLS, U = 8, ROWS = RSTEP * U, NCH = kBwdBN / ROWS;
@@ -331,12 +332,13 @@ template <int D>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_sum_kernel(const AttnParams p) {
   using S = DkvSum<D>;
   constexpr int BN = kBwdBN;
-  const int tile = blockIdx.x / S::NCH, ch = blockIdx.x % S::NCH;
-  if (tile >= *p.nsplit) return;
+  const int units = *p.nsplit * S::NCH;
+  for (int unit = blockIdx.x; unit < units; unit += gridDim.x) {
+  const int tile = unit / S::NCH, ch = unit % S::NCH;
   const SplitTile st = p.splits[tile];
   const SeqInfo si = p.seq[st.b];
   const int hk = blockIdx.y;
-  if ((st.slot0 + st.np) * p.hkv > kSplitSlots) return;
+  if ((st.slot0 + st.np) * p.hkv > kSplitSlots) continue;
   const int col = threadIdx.x % S::COLS, which = col / S::C4, c = col - which * S::C4;
   const int k0 = st.t * BN;
   const int rows = min(BN, si.k_len - k0);
@@ -360,6 +362,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_sum_kernel(const AttnParams 
                            : p.dv + row * p.dv_tok + (int64_t)hk * p.dv_head + 4 * c;
     *reinterpret_cast<bf16x4*>(dst) = bf16x4{(bf16)(acc[u][0] * sc), (bf16)(acc[u][1] * sc), (bf16)(acc[u][2] * sc),
                                              (bf16)(acc[u][3] * sc)};
+  }
   }
 }
 
@@ -544,7 +547,7 @@ hipError_t launch_bwd_t(const AttnParams& p, int qcap, int kvcap, hipStream_t st
   hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)qcap * p.hq)), dim3(256), 0, stream, p);
   hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)kvcap * p.hkv)), dim3(512), 0, stream,
                      p);
-  hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D>), dim3(kMaxSplitTiles * DkvSum<D>::NCH, p.hkv), dim3(256), 0, stream,
+  hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D>), dim3(min(kMaxSplitTiles * DkvSum<D>::NCH, 512), p.hkv), dim3(256), 0, stream,
                      p);
   return hipGetLastError();
 }

@@ -175,10 +175,17 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
   for (int i = tid; i < kSchedKeys; i += kSchedThreads) hist[i] = 0;
   __threadfence_block();
   __syncthreads();
-  // 2: piece length S >= hkv * steps / kSplitTarget, so that the split pieces
-  // (each kv-head counted) number at most 2 kSplitTarget and the items at most
-  // kSplitTarget more than the tiles.
+  // 2: piece length S >= hkv * steps / (2 kSplitTarget), so that the split
+  // pieces (each kv-head counted) number at most 4 kSplitTarget and the items
+  // at most 2 kSplitTarget more than the tiles: S = hkv * steps / kSplitTarget
+  // (about a CU's share of the steps), halved when that is longer than
+  // kLongPiece steps (long pieces amortise their partial sums, and finer ones
+  // balance the CUs better).
   long long sl = (steps * hkv + kSplitTarget - 1) / kSplitTarget;
+  if (sl > kLongPiece) {
+    const long long half = (steps * hkv + 2 * kSplitTarget - 1) / (2 * kSplitTarget);
+    sl = half > kLongPiece ? half : kLongPiece;
+  }
   if (sl < kMinSplitSteps) sl = kMinSplitSteps;
   if (sl > (1 << 30)) sl = 1 << 30;
   const int S = (int)sl;
