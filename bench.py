@@ -4,18 +4,26 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
 One step = one forward + backward of varlen packed attention over the config-2
 batch (Qwen2.5-1.5B heads: 12 q / 2 kv, d 128, 32 lognormal sequences, 16384
-tokens, causal), inputs already resident in HBM.  The headline ``value`` is
-its algorithmic TFLOP/s (12 * d * P * Hq per step, P = allowed (q, k) pairs of
-the realised cu_seqlens; recompute not counted).  The fused lm_head
-cross-entropy (config 4) is timed the same way and reported under ``ce``
-(tokens/s and TFLOP/s at 6 * n * hdim * vocab).
+tokens, causal), inputs already resident in HBM, including the build of the
+batch's schedule (the plan every layer of a packed batch shares; built once
+per step here, so its cost is charged in full to one layer).  The headline
+``value`` is its algorithmic TFLOP/s (12 * d * P * Hq per step, P = allowed
+(q, k) pairs of the realised cu_seqlens; recompute not counted), from the
+median step time.
 
-Timing: HIP events recorded on the stream the kernels are launched on,
-bracketing K steps after W warm-up steps, with device synchronisation on both
-sides; per-call events give each operator's average duration for the
-roofline.  The CPU baseline times the reference path's own library calls
-(oracle/cpu_path.py: SDPA with a block-diagonal mask + repeat_kv, F.linear +
-F.cross_entropy, fp32 autograd) on a bounded sample of the same inputs.
+Every other BASELINE configuration is timed the same way and reported beside
+it: config 3 (SigLIP bidirectional) and config 5 (skewed packing) fwd+bwd,
+config 1 forward (also timed on the host CPU: the reference path's fp32 SDPA
+with a block-diagonal mask), and config 4, the fused lm_head cross-entropy
+(tokens/s over all rows, and TFLOP/s at 6 * n * hdim * vocab over all rows and
+over the rows whose label counts).
+
+Timing: HIP events recorded on the stream the kernels are launched on around
+every step (and every call inside it), W warm-up steps first, device
+synchronisation on both sides; the median over K >= 20 steps is reported.  The
+shader clock is probed right after the timed steps (``gpu_clock_mhz``).  The
+CPU baseline times the reference path's own library calls
+(oracle/cpu_path.py) on bounded samples of the same inputs.
 """
 
 from __future__ import annotations
@@ -29,6 +37,7 @@ import time
 
 import torch
 
+from siq_vl_amd import _lib
 from siq_vl_amd import attention as A
 from siq_vl_amd import cross_entropy as C
 from siq_vl_amd import projector as PJ
@@ -38,7 +47,9 @@ from siq_vl_amd import workloads as W
 
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CUs x 2.4 GHz)
 PEAK_HBM_GBS = 8000.0
+PEAK_CLOCK_MHZ = 2400.0
 COPY_BYTES = 256 << 20
+MIN_STEPS = 20
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
 
 
@@ -50,6 +61,8 @@ def measured_traffic(key: str):
             return int(json.load(fh)[key]["bytes_per_call"])
     except (OSError, KeyError, ValueError):
         return None
+
+
 METRIC = "packed varlen attn fwd+bwd TFLOP/s (% bf16 MFMA peak); fused-CE tokens/s"
 
 
@@ -57,60 +70,111 @@ def _events(n):
     return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
 
-def bench_attention(steps: int, warmup: int) -> dict:
-    cfg = W.attn_config(2)
+def _median(a):
+    a = sorted(a)
+    n = len(a)
+    return a[n // 2] if n % 2 else 0.5 * (a[n // 2 - 1] + a[n // 2])
+
+
+def probe_clock_mhz() -> float | None:
+    """Shader clock right now (MHz), from the library's clock probe (~200 us of spinning)."""
+    out = torch.zeros(2, dtype=torch.int64, device="cuda")
+    rc = _lib.lib().siq_probe_clock(out.data_ptr(), 20000, torch.cuda.current_stream().cuda_stream)
+    if rc != 0:
+        return None
+    cyc, ticks = (int(x) for x in out.cpu().tolist())
+    return 100.0 * cyc / ticks if ticks > 0 else None
+
+
+def timed_steps(parts, steps: int, warmup: int) -> dict:
+    """Runs ``parts`` (list of (name, fn)) in order as one step, ``warmup`` times
+    untimed, then ``steps`` times with events on the launch stream around every
+    part.  Returns median / mean step ms and median ms per part."""
+    for _ in range(warmup):
+        for _, fn in parts:
+            fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    np_ = len(parts)
+    ev = _events(steps * np_ + 1)
+    ev[0].record(stream)
+    for i in range(steps):
+        for j, (_, fn) in enumerate(parts):
+            fn()
+            ev[i * np_ + j + 1].record(stream)
+    torch.cuda.synchronize()
+    per_step = [ev[i * np_].elapsed_time(ev[(i + 1) * np_]) for i in range(steps)]
+    res = {"median_ms": _median(per_step), "mean_ms": ev[0].elapsed_time(ev[-1]) / steps, "steps": steps}
+    for j, (name, _) in enumerate(parts):
+        res[name + "_ms"] = _median([ev[i * np_ + j].elapsed_time(ev[i * np_ + j + 1]) for i in range(steps)])
+    return res
+
+
+def bench_attention(idx: int, steps: int, warmup: int) -> dict:
+    """Config ``idx``: plan + forward (+ backward when the config has one) per step."""
+    cfg = W.attn_config(idx)
     dev = torch.device("cuda")
     x = W.attn_inputs(cfg, device=dev)
     cu = cfg.cu_seqlens().to(dev)
     scale = cfg.d**-0.5
     mx = cfg.max_seqlen
+    st = {}
 
-    def step():
-        out, lse = A.varlen_attn_fwd(x["q"], x["k"], x["v"], cu, cu, mx, mx, scale, True)
-        dq, dk, dv = A.varlen_attn_bwd(x["dout"], x["q"], x["k"], x["v"], out, lse, cu, cu, mx, mx, scale, True)
-        return out, lse, dq, dk, dv
+    def plan():
+        st["plan"] = A.build_attn_plan(cu, cu, cfg.total, cfg.total, cfg.hq, cfg.hkv, cfg.causal, dev)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    ev = _events(3 * steps + 2)
-    # operator-level events: [fwd start, fwd end / bwd start, bwd end] per step
-    ev[0].record(stream)
-    for i in range(steps):
-        ev[1 + 3 * i].record(stream)
-        out, lse = A.varlen_attn_fwd(x["q"], x["k"], x["v"], cu, cu, mx, mx, scale, True)
-        ev[2 + 3 * i].record(stream)
-        A.varlen_attn_bwd(x["dout"], x["q"], x["k"], x["v"], out, lse, cu, cu, mx, mx, scale, True)
-        ev[3 + 3 * i].record(stream)
-    ev[-1].record(stream)
-    torch.cuda.synchronize()
-    total_ms = ev[0].elapsed_time(ev[-1])
-    fwd_ms = sorted(ev[1 + 3 * i].elapsed_time(ev[2 + 3 * i]) for i in range(steps))
-    bwd_ms = sorted(ev[2 + 3 * i].elapsed_time(ev[3 + 3 * i]) for i in range(steps))
-    med = lambda a: a[len(a) // 2]
+    def fwd():
+        st["out"], st["lse"] = A.varlen_attn_fwd(x["q"], x["k"], x["v"], cu, cu, mx, mx, scale, cfg.causal,
+                                                 plan=st["plan"])
+
+    def bwd():
+        A.varlen_attn_bwd(x["dout"], x["q"], x["k"], x["v"], st["out"], st["lse"], cu, cu, mx, mx, scale,
+                          cfg.causal, plan=st["plan"])
+
+    parts = [("plan", plan), ("fwd", fwd)] + ([("bwd", bwd)] if cfg.backward else [])
+    r = timed_steps(parts, steps, warmup)
     pairs = cfg.pairs()
     flops_fwd = 4.0 * cfg.d * pairs * cfg.hq
-    flops_bwd = 8.0 * cfg.d * pairs * cfg.hq
-    ms_step = total_ms / steps
-    # algorithmic bytes of one step: read q,k,v (fwd) + q,k,v,o,do,lse (bwd), write o,lse,dq,dk,dv
+    flops_bwd = 8.0 * cfg.d * pairs * cfg.hq if cfg.backward else 0.0
     t, hq, hkv, d = cfg.total, cfg.hq, cfg.hkv, cfg.d
     qb, kvb, lseb = t * hq * d * 2, t * hkv * d * 2, t * hq * 4
+    # algorithmic bytes: read q,k,v (fwd) + q,k,v,o,do,lse (bwd); write o,lse (fwd) + dq,dk,dv (bwd)
     bytes_fwd = qb + 2 * kvb + qb + lseb
     bytes_bwd = 3 * qb + 2 * kvb + lseb + qb + 2 * kvb
-    return {
-        "cfg": cfg,
-        "ms_per_step": ms_step,
-        "tflops": (flops_fwd + flops_bwd) / (ms_step * 1e-3) / 1e12,
-        "fwd_ms": med(fwd_ms),
-        "bwd_ms": med(bwd_ms),
-        "fwd_tflops": flops_fwd / (med(fwd_ms) * 1e-3) / 1e12,
-        "bwd_tflops": flops_bwd / (med(bwd_ms) * 1e-3) / 1e12,
-        "flops_bwd": flops_bwd,
-        "bytes": bytes_fwd + bytes_bwd,
-        "bytes_bwd": bytes_bwd,
-        "pairs": pairs,
+    ms = r["median_ms"]
+    out = {
+        "cfg": cfg, "pairs": pairs, "ms_per_step": ms, "mean_ms_per_step": r["mean_ms"],
+        "plan_ms": r["plan_ms"], "fwd_ms": r["fwd_ms"],
+        "tflops": (flops_fwd + flops_bwd) / (ms * 1e-3) / 1e12,
+        "fwd_tflops": flops_fwd / (r["fwd_ms"] * 1e-3) / 1e12,
+        "flops_fwd": flops_fwd, "flops_bwd": flops_bwd, "bytes_fwd": bytes_fwd, "bytes_bwd": bytes_bwd,
     }
+    if cfg.backward:
+        out["bwd_ms"] = r["bwd_ms"]
+        out["bwd_tflops"] = flops_bwd / (r["bwd_ms"] * 1e-3) / 1e12
+    return out
+
+
+def attn_block(a: dict) -> dict:
+    """The JSON block of one attention config."""
+    cfg = a["cfg"]
+    blk = {"workload": cfg.name, "total_tokens": cfg.total, "sequences": len(cfg.lengths),
+           "max_seqlen": cfg.max_seqlen, "heads": f"{cfg.hq}/{cfg.hkv}", "head_dim": cfg.d, "causal": cfg.causal,
+           "pairs": a["pairs"], "ms_per_step": round(a["ms_per_step"], 4),
+           "mean_ms_per_step": round(a["mean_ms_per_step"], 4), "plan_us": round(a["plan_ms"] * 1e3, 2),
+           "fwd_ms": round(a["fwd_ms"], 4), "fwd_tflops": round(a["fwd_tflops"], 2),
+           "tflops": round(a["tflops"], 2), "pct_bf16_peak": round(100.0 * a["tflops"] / PEAK_BF16_TFLOPS, 2)}
+    if cfg.backward:
+        blk["bwd_ms"] = round(a["bwd_ms"], 4)
+        blk["bwd_tflops"] = round(a["bwd_tflops"], 2)
+        ach = (a["flops_fwd"] + a["flops_bwd"]) / ((a["fwd_ms"] + a["bwd_ms"]) * 1e-3) / 1e12
+        blk["roofline"] = {"bound": "mfma", "kernel": "forward + backward calls", "achieved": round(ach, 2),
+                           "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4)}
+    else:
+        blk["roofline"] = {"bound": "mfma", "kernel": "forward call", "achieved": round(a["fwd_tflops"], 2),
+                           "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                           "frac": round(a["fwd_tflops"] / PEAK_BF16_TFLOPS, 4)}
+    return blk
 
 
 def _rope_inputs(cfg, dev):
@@ -298,51 +362,45 @@ def bench_splice(steps: int, warmup: int) -> dict:
             "gbs": nbytes / (fwd_ms * 1e-3) / 1e9}
 
 
-def bench_ce(steps: int, warmup: int, chunk: int) -> dict:
+def bench_ce(steps: int, warmup: int, chunk: int | None) -> dict:
     cfg = W.CONFIG4
     dev = torch.device("cuda")
     x = W.ce_inputs(cfg, device=dev)
+    chunk = C.default_chunk_tokens(cfg.vocab) if chunk is None else chunk
 
     def step():
         return C.flce_fwd_bwd(x["hidden"], x["weight"], x["labels"], chunk_tokens=chunk)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    ev = _events(steps + 1)
-    ev[0].record(stream)
-    for i in range(steps):
-        step()
-        ev[i + 1].record(stream)
-    torch.cuda.synchronize()
-    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
-    ms = ev[0].elapsed_time(ev[-1]) / steps
-    # tokens/s counts every row of the batch (the metric); TFLOP/s counts the
-    # work the kernels execute: rows whose label is ignored are compacted out
-    # before the logits GEMM, so 6 H V FLOP per row with a label that counts
+    r = timed_steps([("ce", step)], steps, warmup)
+    ms = r["median_ms"]
+    # tokens/s counts every row of the batch (the metric); the executed TFLOP/s counts the work the
+    # kernels run: rows whose label is ignored are compacted out before the logits GEMM
     n_valid = int(((x["labels"] != C.IGNORE_INDEX) & (x["labels"] >= 0) & (x["labels"] < cfg.vocab)).sum())
+    ws = C.flce_workspace_bytes(cfg.n, cfg.hdim, cfg.vocab, chunk, True)
     return {
-        "cfg": cfg,
-        "ms_per_step": ms,
-        "median_ms": per[len(per) // 2],
-        "tokens_per_s": cfg.n / (ms * 1e-3),
-        "n_valid": n_valid,
-        "tflops": 6.0 * n_valid * cfg.hdim * cfg.vocab / (ms * 1e-3) / 1e12,
-        "chunk": chunk,
+        "cfg": cfg, "ms_per_step": ms, "mean_ms_per_step": r["mean_ms"],
+        "tokens_per_s": cfg.n / (ms * 1e-3), "n_valid": n_valid,
+        "tflops_all_rows": 6.0 * cfg.n * cfg.hdim * cfg.vocab / (ms * 1e-3) / 1e12,
+        "tflops_executed": 6.0 * n_valid * cfg.hdim * cfg.vocab / (ms * 1e-3) / 1e12,
+        "chunk": chunk, "workspace_bytes": ws,
+        "e_bytes": 2 * chunk * cfg.vocab,
+        "algorithmic_bytes": 2 * (2 * cfg.n * cfg.hdim + 2 * cfg.vocab * cfg.hdim) + 8 * cfg.n,
     }
 
 
-def cpu_baseline(budget_s: float = 20.0) -> dict:
-    """Reference path (oracle/cpu_path.py) on the host cores, bounded sample."""
-    from oracle import cpu_path
-
+def _cpu_threads() -> int:
     # the host share this GPU's job may use (OMP_NUM_THREADS on the GPU box), never above the core count
     cores = os.cpu_count() or 1
-    threads = min(cores, int(os.environ.get("OMP_NUM_THREADS") or cores))
-    torch.set_num_threads(threads)
+    return min(cores, int(os.environ.get("OMP_NUM_THREADS") or cores))
+
+
+def cpu_baseline(budget_s: float = 20.0) -> dict:
+    """Reference path (oracle/cpu_path.py) on the host cores, bounded samples."""
+    from oracle import cpu_path
+
+    torch.set_num_threads(_cpu_threads())
     res = {}
-    # attention: the first sequences of the config-2 batch, ~2048 tokens
+    # config 2 (headline): the first sequences of the batch, ~2048 tokens, fwd+bwd
     cfg = W.attn_config(2)
     lens = []
     for n in cfg.lengths:
@@ -362,13 +420,32 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
         out = cpu_path.sdpa_attention(q, k, v, cu, cfg.d**-0.5, True)
         out.backward(do)
         reps += 1
-        if time.perf_counter() - t0 > budget_s / 2 or reps >= 50:
+        if time.perf_counter() - t0 > budget_s * 0.4 or reps >= 50:
             break
     dt = (time.perf_counter() - t0) / reps
     res["attn"] = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
                    "kind": "port",
                    "sample": f"config-2 first {len(lens)} sequences ({sum(lens)} tokens), fp32 SDPA + block-diagonal "
                              f"mask + repeat_kv, fwd+bwd autograd, {reps} reps"}
+    # config 1 (CPU-reported in the baseline): the whole batch, forward only
+    c1 = W.attn_config(1)
+    x1 = W.attn_inputs(c1, device="cpu")
+    cu1 = c1.cu_seqlens().tolist()
+    q1, k1, v1 = (x1[n].float() for n in ("q", "k", "v"))
+    flops1 = 4.0 * c1.d * c1.pairs() * c1.hq
+    t0 = time.perf_counter()
+    reps = 0
+    with torch.no_grad():
+        while True:
+            cpu_path.sdpa_attention(q1, k1, v1, cu1, c1.d**-0.5, True)
+            reps += 1
+            if time.perf_counter() - t0 > budget_s * 0.3 or reps >= 20:
+                break
+    dt1 = (time.perf_counter() - t0) / reps
+    res["attn_config1"] = {"value": flops1 / dt1 / 1e12, "unit": "TFLOP/s", "ms": dt1 * 1e3,
+                           "cores": torch.get_num_threads(), "kind": "port",
+                           "sample": f"config 1 whole batch ({c1.total} tokens, 8 sequences, 14/2 heads, d 64), fp32 "
+                                     f"SDPA + block-diagonal causal mask + repeat_kv, forward, {reps} reps"}
     # CE: 256 rows of config 4 against the full vocabulary
     c4 = W.CONFIG4
     g = torch.Generator().manual_seed(W.SEED)
@@ -382,7 +459,7 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
         loss = cpu_path.cross_entropy(h, w, y)
         loss.backward()
         reps += 1
-        if time.perf_counter() - t0 > budget_s / 2 or reps >= 20:
+        if time.perf_counter() - t0 > budget_s * 0.3 or reps >= 20:
             break
     dt = (time.perf_counter() - t0) / reps
     res["ce"] = {"value": n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
@@ -397,12 +474,14 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--ce-chunk", type=int, default=C.DEFAULT_CHUNK_TOKENS)
+    ap.add_argument("--ce-chunk", type=int, default=None,
+                    help="CE token rows per logits chunk (default: the 2 GiB bound on the chunk's numerators)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-ce", action="store_true")
     ap.add_argument("--skip-rope", action="store_true")
     ap.add_argument("--skip-projector", action="store_true")
     ap.add_argument("--skip-splice", action="store_true")
+    ap.add_argument("--attn-only", action="store_true", help="attention configs only (no CE / widening legs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (3 times): the known-size reference that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -423,34 +502,50 @@ def main() -> int:
         torch.cuda.synchronize()
         print(f"[bench] copied {COPY_BYTES} bytes 3 times", file=sys.stderr, flush=True)
         return 0
+    if args.attn_only:
+        args.skip_ce = args.skip_rope = args.skip_projector = args.skip_splice = True
 
-    att = bench_attention(args.steps, args.warmup)
-    print(f"[bench] attention fwd+bwd {att['ms_per_step']:.3f} ms/step, {att['tflops']:.1f} TFLOP/s "
-          f"(fwd {att['fwd_ms']:.3f} ms, bwd {att['bwd_ms']:.3f} ms)", file=sys.stderr, flush=True)
+    # the headline leg first, then the other configurations (all >= MIN_STEPS timed steps)
+    steps = max(args.steps, 1)
+    leg_steps = max(steps, MIN_STEPS)
+    att = bench_attention(2, steps, args.warmup)
+    clock = probe_clock_mhz()
+    print(f"[bench] config 2 attention fwd+bwd {att['ms_per_step']:.4f} ms/step (median), {att['tflops']:.1f} "
+          f"TFLOP/s (plan {att['plan_ms'] * 1e3:.1f} us, fwd {att['fwd_ms'] * 1e3:.1f} us, bwd "
+          f"{att['bwd_ms'] * 1e3:.1f} us); shader clock after {clock} MHz", file=sys.stderr, flush=True)
+    others = {}
+    for idx in (3, 5, 1):
+        others[idx] = bench_attention(idx, leg_steps, args.warmup)
+        o = others[idx]
+        extra = f", bwd {o['bwd_ms'] * 1e3:.1f} us" if "bwd_ms" in o else ""
+        print(f"[bench] config {idx} attention {o['ms_per_step']:.4f} ms/step, {o['tflops']:.1f} TFLOP/s (fwd "
+              f"{o['fwd_ms'] * 1e3:.1f} us{extra})", file=sys.stderr, flush=True)
     ce = None
     if not args.skip_ce:
-        ce = bench_ce(max(3, args.steps // 4), min(args.warmup, 2), args.ce_chunk)
-        print(f"[bench] fused CE {ce['ms_per_step']:.3f} ms/step, {ce['tokens_per_s']:.3e} tokens/s, "
-              f"{ce['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+        ce = bench_ce(leg_steps, args.warmup, args.ce_chunk)
+        print(f"[bench] config 4 fused CE {ce['ms_per_step']:.3f} ms/step (median), {ce['tokens_per_s']:.3e} tokens/s, "
+              f"{ce['tflops_all_rows']:.1f} TFLOP/s over all rows, {ce['tflops_executed']:.1f} executed "
+              f"(chunk {ce['chunk']} rows)", file=sys.stderr, flush=True)
     rope = None
     if not args.skip_rope:
-        rope = bench_rope(max(10, args.steps), args.warmup)
+        rope = bench_rope(leg_steps, args.warmup)
         print(f"[bench] fused RoPE fwd {rope['fwd_ms'] * 1e3:.1f} us ({rope['fwd_gbs']:.0f} GB/s), bwd "
               f"{rope['bwd_ms'] * 1e3:.1f} us ({rope['bwd_gbs']:.0f} GB/s) in a graph; one eager call "
               f"{rope['eager_fwd_ms'] * 1e3:.1f} us; reference torch ops fwd+bwd {rope['ref_ms'] * 1e3:.1f} us",
               file=sys.stderr, flush=True)
     proj = None
     if not args.skip_projector:
-        proj = bench_projector(max(10, args.steps), args.warmup)
+        proj = bench_projector(leg_steps, args.warmup)
         print(f"[bench] projector fwd {proj['fwd_ms'] * 1e3:.1f} us ({proj['fwd_tflops']:.0f} TFLOP/s), bwd "
               f"{proj['bwd_ms'] * 1e3:.1f} us ({proj['bwd_tflops']:.0f} TFLOP/s); reference torch ops fwd+bwd "
               f"{proj['ref_ms'] * 1e3:.1f} us", file=sys.stderr, flush=True)
     spl = None
     if not args.skip_splice:
-        spl = bench_splice(max(10, args.steps), args.warmup)
+        spl = bench_splice(leg_steps, args.warmup)
         print(f"[bench] splice kernels {spl['fwd_ms'] * 1e3:.1f} us ({spl['gbs']:.0f} GB/s), whole op with its count "
               f"check {spl['op_ms'] * 1e3:.1f} us; reference torch ops {spl['ref_ms'] * 1e3:.1f} us",
               file=sys.stderr, flush=True)
+    clock_end = probe_clock_mhz()
     cpu = None if args.no_cpu_baseline else cpu_baseline()
 
     cfg = att["cfg"]
@@ -460,7 +555,7 @@ def main() -> int:
         "value": round(att["tflops"], 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(att["ms_per_step"], 4),
         "higher_is_better": True,
@@ -469,24 +564,44 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) bf16, lognormal lengths; no checkpoint)",
         "config": {"workload": "config 2: varlen causal GQA attention fwd+bwd, Qwen2.5-1.5B heads "
-                               "(12 q / 2 kv, d 128), 32 lognormal(400, 0.75) sequences, 16384 tokens",
+                               "(12 q / 2 kv, d 128), 32 lognormal(400, 0.75) sequences, 16384 tokens; "
+                               "step = plan build + forward + backward, median of the timed steps",
                    "total_tokens": cfg.total, "max_seqlen": cfg.max_seqlen, "pairs": att["pairs"],
                    "pct_bf16_peak": round(100.0 * att["tflops"] / PEAK_BF16_TFLOPS, 2),
+                   "mean_ms_per_step": round(att["mean_ms_per_step"], 4),
+                   "plan_us": round(att["plan_ms"] * 1e3, 2),
                    "fwd_ms": round(att["fwd_ms"], 4), "bwd_ms": round(att["bwd_ms"], 4),
                    "fwd_tflops": round(att["fwd_tflops"], 2), "bwd_tflops": round(att["bwd_tflops"], 2)},
-        "roofline": {"bound": "mfma", "kernel": "attention backward call (schedule + dQ + dK/dV + split-tile sum kernels)",
+        "roofline": {"bound": "mfma", "kernel": "attention backward call (dQ + dK/dV + split-tile sum kernels) "
+                                               "over the batch's plan",
                      "achieved": round(bwd_achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(bwd_achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": measured_traffic("attention_bwd_config2"),
                      "algorithmic_bytes": att["bytes_bwd"]},
         "cpu_baseline": cpu["attn"] if cpu else None,
+        "gpu_clock_mhz": {"after_headline": None if clock is None else round(clock, 1),
+                          "at_end": None if clock_end is None else round(clock_end, 1),
+                          "peak_quoted_at": PEAK_CLOCK_MHZ,
+                          "method": "siq_probe_clock: shader-clock counter over the 100 MHz counter, one wave per CU"},
+        "attention_configs": {str(i): attn_block(o) for i, o in [(2, att)] + sorted(others.items())},
     }
+    if cpu:
+        line["attention_configs"]["1"]["cpu_baseline"] = cpu["attn_config1"]
     if ce is not None:
         line["ce"] = {"workload": "config 4: fused linear CE fwd+bwd, h [16384,1536], W [151936,1536], 30% span mask",
                       "tokens_per_s": round(ce["tokens_per_s"], 1), "ms_per_step": round(ce["ms_per_step"], 4),
-                      "tflops": round(ce["tflops"], 2), "tflops_rows": ce["n_valid"],
-                      "pct_bf16_peak": round(100.0 * ce["tflops"] / PEAK_BF16_TFLOPS, 2),
-                      "chunk_tokens": ce["chunk"],
+                      "mean_ms_per_step": round(ce["mean_ms_per_step"], 4),
+                      "tflops_all_rows": round(ce["tflops_all_rows"], 2),
+                      "pct_bf16_peak_all_rows": round(100.0 * ce["tflops_all_rows"] / PEAK_BF16_TFLOPS, 2),
+                      "tflops_executed": round(ce["tflops_executed"], 2), "rows_with_label": ce["n_valid"],
+                      "chunk_tokens": ce["chunk"], "numerator_buffer_bytes": ce["e_bytes"],
+                      "workspace_bytes": ce["workspace_bytes"],
+                      "roofline": {"bound": "mfma", "kernel": "siq_flce_fwd_bwd call (all kernels)",
+                                   "achieved": round(ce["tflops_executed"], 2), "peak": PEAK_BF16_TFLOPS,
+                                   "unit": "TFLOP/s", "frac": round(ce["tflops_executed"] / PEAK_BF16_TFLOPS, 4),
+                                   "work": "6 * rows_with_label * hdim * vocab",
+                                   "traffic": measured_traffic("ce_config4"),
+                                   "algorithmic_bytes": ce["algorithmic_bytes"]},
                       "cpu_baseline": cpu["ce"] if cpu else None}
     if rope is not None:
         line["rope"] = {"workload": "config-2 shape: RoPE of q [16384,12,128] and k [16384,2,128] (Qwen2 layout, "

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define SIQ_ABI_VERSION 1
+#define SIQ_ABI_VERSION 2
 
 enum siq_status {
   SIQ_OK = 0,
@@ -100,6 +100,42 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
                         float softmax_scale, int causal, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Attention plans: the schedule of one packed batch, built once and reused.
+ *
+ * The reference forwards the same cu_seq_lens_* kwargs to every decoder layer
+ * (siq_vl/model/modeling.py:278-288 -> transformers modeling_qwen2.py:216-230),
+ * so the work lists siq_attn_varlen_fwd / _bwd build on every call (sequence
+ * extents, q tiles and dK/dV work items ordered by decreasing work) are the
+ * same for all layers.  siq_attn_build_plan writes them once into `plan`
+ * (siq_attn_plan_bytes, device memory owned by the caller); the *_plan entry
+ * points then run the forward / backward of any layer over it.  A plan
+ * depends on the offsets, total_q / total_k, hq / hkv and causal only; it
+ * records them, and a kernel handed a plan built for other values writes
+ * nothing and sets a mismatch bit in the plan (bytes 48..51, int32) instead of
+ * touching memory outside its tensors.  Bytes 40..47 hold the scheduler's
+ * overflow bits (0 by construction).
+ * ------------------------------------------------------------------------- */
+size_t siq_attn_plan_bytes(int batch, int64_t total_q, int64_t total_k);
+
+int siq_attn_build_plan(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch, int64_t total_q,
+                        int64_t total_k, int hq, int hkv, int causal, void* plan, size_t plan_bytes, void* stream);
+
+/* siq_attn_varlen_fwd over a built plan (no workspace). */
+int siq_attn_varlen_fwd_plan(const void* q, const void* k, const void* v, void* o, float* lse, int batch,
+                             int64_t total_q, int64_t total_k, int hq, int hkv, int d, const int64_t* strides,
+                             float softmax_scale, int causal, const void* plan, size_t plan_bytes, void* stream);
+
+/* siq_attn_varlen_bwd over a built plan; the workspace holds the backward's
+ * own scratch only (siq_attn_bwd_plan_workspace_bytes). */
+size_t siq_attn_bwd_plan_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d);
+
+int siq_attn_varlen_bwd_plan(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                             const void* dout, void* dq, void* dk, void* dv, int batch, int64_t total_q,
+                             int64_t total_k, int hq, int hkv, int d, const int64_t* strides, float softmax_scale,
+                             int causal, const void* plan, size_t plan_bytes, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Fused linear cross-entropy (lm_head + loss), forward and backward.
  *
  * Replaces logits = lm_head(h) (transformers models/qwen2/modeling_qwen2.py:
@@ -108,7 +144,7 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
  * backward.  hidden [n, hdim] bf16 row-major, weight [vocab, hdim] bf16
  * row-major, labels [n] int64 (already shifted; ignore_index rows are skipped;
  * any other value outside [0, vocab) is treated as ignored and counted in
- * *bad_labels).
+ * *bad_labels, which the host raises on as F.cross_entropy would).
  *
  * reduction 0 ("mean"): loss = sum_valid(lse - z_y) / count_valid.
  * reduction 1 ("sum" then divide, as with num_items_in_batch):
@@ -120,7 +156,10 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
  *
  * The logits are produced chunk_tokens rows at a time: only the softmax
  * numerators of one chunk (chunk_tokens x vocab bf16, each relative to the max
- * of its 256-column tile) ever exist, in the workspace.
+ * of its 256-column tile) ever exist, in the workspace; chunks count rows
+ * whose label counts (ignored rows are compacted away first).  With more than
+ * one chunk dweight is summed over chunks in an fp32 [vocab, hdim] workspace
+ * buffer.
  * ------------------------------------------------------------------------- */
 size_t siq_flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk_tokens, int need_dweight);
 
@@ -129,10 +168,26 @@ int siq_flce_fwd_bwd(const void* hidden, const void* weight, const int64_t* labe
                      int64_t* count, int64_t* bad_labels, void* dhidden, void* dweight, int64_t chunk_tokens,
                      void* workspace, size_t workspace_bytes, void* stream);
 
-/* Multiplies a bf16 buffer in place by a device fp32 scalar (a no-op when the
- * scalar is exactly 1.0): applies the upstream gradient of the scalar loss to
- * dhidden / dweight.  Companion of siq_flce_fwd_bwd; no reference
- * counterpart (autograd's chain rule). */
+/* Loss only: the same loss, count and bad_labels as siq_flce_fwd_bwd on the
+ * same inputs (bitwise), without the gradient work -- the reference's
+ * evaluation pass (scripts/train.py:693-699 evaluates eval_loss under
+ * torch.no_grad through the same lm_head + ForCausalLMLoss call).  Only the
+ * logits GEMM and the chunked logsumexp run; no softmax numerators are
+ * stored.  Workspace: siq_flce_loss_workspace_bytes. */
+size_t siq_flce_loss_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab);
+
+int siq_flce_loss(const void* hidden, const void* weight, const int64_t* labels, int64_t n, int64_t hdim,
+                  int64_t vocab, int64_t ignore_index, int reduction, const float* divisor, float* loss,
+                  int64_t* count, int64_t* bad_labels, void* workspace, size_t workspace_bytes, void* stream);
+
+/* dst = src * (*scalar) over numel bf16 elements, rounded once from fp32
+ * (a device fp32 scalar, read on the device): applies the upstream gradient
+ * of the scalar loss to dhidden / dweight.  Companion of siq_flce_fwd_bwd; no
+ * reference counterpart (autograd's chain rule).  src == dst scales in place
+ * (and then an exact 1.0 writes nothing); any other overlap is undefined. */
+int siq_scale_bf16(const void* src, void* dst, int64_t numel, const float* scalar, void* stream);
+
+/* siq_scale_bf16(data, data, numel, scalar, stream). */
 int siq_scale_bf16_inplace(void* data, int64_t numel, const float* scalar, void* stream);
 
 /* ---------------------------------------------------------------------------
@@ -218,6 +273,16 @@ int siq_splice_fwd(const int64_t* input_ids, int64_t n_tokens, const void* weigh
                    int64_t* counts, void* workspace, size_t workspace_bytes, void* stream);
 
 int siq_gather_rows(const void* src, const int32_t* rows, int64_t n, int64_t hidden, void* dst, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Measurement support (no reference counterpart).
+ *
+ * siq_probe_clock: one wave per CU spins for about spin_ticks ticks of the
+ * constant 100 MHz counter and writes out[0] = shader-clock cycles elapsed,
+ * out[1] = 100 MHz ticks elapsed (device uint64[2]); the shader clock the GPU
+ * ran at is out[0] / out[1] * 100 MHz.  spin_ticks in [1, 1e8].
+ * ------------------------------------------------------------------------- */
+int siq_probe_clock(uint64_t* out, int64_t spin_ticks, void* stream);
 
 #ifdef __cplusplus
 }

@@ -45,12 +45,34 @@ _PROTOS = {
          _c_void_p, _c_void_p, _i32, _i32, _i32, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_i64), _f32, _i32,
          _c_void_p, _size, _c_void_p],
     ),
+    "siq_attn_plan_bytes": (_size, [_i32, _i64, _i64]),
+    "siq_attn_bwd_plan_workspace_bytes": (_size, [_i32, _i64, _i64, _i32, _i32, _i32]),
+    "siq_attn_build_plan": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _i64, _i32, _i32, _i32, _c_void_p, _size,
+                                   _c_void_p]),
+    "siq_attn_varlen_fwd_plan": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i64, _i32, _i32, _i32,
+         ctypes.POINTER(_i64), _f32, _i32, _c_void_p, _size, _c_void_p],
+    ),
+    "siq_attn_varlen_bwd_plan": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _i32, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_i64), _f32, _i32, _c_void_p, _size, _c_void_p, _size,
+         _c_void_p],
+    ),
     "siq_flce_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i32]),
     "siq_flce_fwd_bwd": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p,
          _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _size, _c_void_p],
     ),
+    "siq_flce_loss_workspace_bytes": (_size, [_i64, _i64, _i64]),
+    "siq_flce_loss": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _size, _c_void_p],
+    ),
+    "siq_scale_bf16": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p]),
     "siq_scale_bf16_inplace": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p]),
     "siq_proj_workspace_bytes": (_size, [_i64, _i64, _i64, _i32, _i64]),
     "siq_proj_fwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _i64, _c_void_p, _size,
@@ -61,6 +83,7 @@ _PROTOS = {
     "siq_splice_fwd": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
                               _c_void_p, _c_void_p, _size, _c_void_p]),
     "siq_gather_rows": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
+    "siq_probe_clock": (_i32, [_c_void_p, _i64, _c_void_p]),
     "siq_rope_fwd": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32, _i32, _i32,

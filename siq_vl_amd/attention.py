@@ -3,7 +3,10 @@
 Three layers, all ending in the HIP kernels behind ``include/siq_kernels.h``:
 
 * ``varlen_attn_fwd`` / ``varlen_attn_bwd`` -- raw operators (validation,
-  workspace, stream) over ``siq_attn_varlen_fwd`` / ``siq_attn_varlen_bwd``.
+  workspace, stream) over ``siq_attn_varlen_fwd_plan`` /
+  ``siq_attn_varlen_bwd_plan``, with the batch's schedule (``AttnPlan``,
+  ``siq_attn_build_plan``) built once per ``cu_seqlens`` tensor and reused by
+  every layer's forward and backward.
 * ``flash_attn_varlen_func`` -- the autograd op with the varlen call
   convention transformers uses for packed batches
   (transformers modeling_flash_attention_utils.py:796-822:
@@ -23,6 +26,7 @@ causal / padding mask, GQA with q-head ``h`` reading kv-head
 
 from __future__ import annotations
 
+import weakref
 from typing import Any
 
 import torch
@@ -112,37 +116,116 @@ def _check_common(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> tuple[in
     return hq, hkv, d
 
 
+# --------------------------------------------------------------------------- plans
+class AttnPlan:
+    """The kernels' schedule of one packed batch (``siq_attn_build_plan``):
+    per-sequence extents, the q-tile list of the forward / dQ kernels and the
+    dK/dV work items, ordered by decreasing work.  It depends only on the
+    sequences, the head counts and causality, so one plan serves the forward
+    and backward of every layer of a packed batch (the reference forwards the
+    same ``cu_seq_lens_*`` kwargs to each decoder layer,
+    siq_vl/model/modeling.py:278-288)."""
+
+    __slots__ = ("buf", "batch", "total_q", "total_k", "hq", "hkv", "causal", "cu_q", "cu_k", "__weakref__")
+
+    def __init__(self, buf, batch, total_q, total_k, hq, hkv, causal, cu_q, cu_k):
+        self.buf, self.batch, self.total_q, self.total_k = buf, batch, total_q, total_k
+        self.hq, self.hkv, self.causal, self.cu_q, self.cu_k = hq, hkv, causal, cu_q, cu_k
+
+    def matches(self, batch: int, total_q: int, total_k: int, hq: int, hkv: int, causal: bool) -> bool:
+        return (self.batch, self.total_q, self.total_k, self.hq // self.hkv, self.hkv, self.causal) == (
+            batch, total_q, total_k, hq // hkv, hkv, bool(causal))
+
+    def status(self) -> dict:
+        """The plan header's status words (one device-to-host read; for tests
+        and debugging): overflow bits of the scheduler, mismatch bits of the
+        kernels that were handed this plan."""
+        words = self.buf[:64].view(torch.int32).cpu().tolist()
+        return {"magic": words[4], "status_q": words[10], "status_kv": words[11], "status_use": words[12]}
+
+
+def build_attn_plan(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, total_q: int, total_k: int, hq: int,
+                    hkv: int, causal: bool, device: torch.device | None = None) -> AttnPlan:
+    """Builds a plan on the device (one small kernel, no host sync)."""
+    device = device or (cu_seqlens_q.device if cu_seqlens_q.device.type == "cuda" else torch.device("cuda"))
+    cu_q = _device_cu(cu_seqlens_q, device, total_q, "cu_seqlens_q")
+    cu_k = _device_cu(cu_seqlens_k, device, total_k, "cu_seqlens_k")
+    if cu_q.numel() != cu_k.numel():
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must describe the same number of sequences")
+    if hq <= 0 or hkv <= 0 or hq % hkv:
+        raise ValueError(f"num q heads ({hq}) must be a positive multiple of num kv heads ({hkv})")
+    batch = cu_q.numel() - 1
+    L = _lib.lib()
+    nbytes = L.siq_attn_plan_bytes(batch, total_q, total_k)
+    buf = torch.empty((max(nbytes, 256),), dtype=torch.uint8, device=device)
+    if batch > 0:
+        rc = L.siq_attn_build_plan(cu_q.data_ptr(), cu_k.data_ptr(), batch, total_q, total_k, hq, hkv,
+                                   int(bool(causal)), buf.data_ptr(), buf.numel(), _stream(device))
+        _lib.check(rc, "siq_attn_build_plan")
+    return AttnPlan(buf, batch, int(total_q), int(total_k), int(hq), int(hkv), bool(causal), cu_q, cu_k)
+
+
+_PLAN_ATTR = "_siq_attn_plans"
+
+
+def cached_attn_plan(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, total_q: int, total_k: int, hq: int,
+                     hkv: int, causal: bool, device: torch.device) -> AttnPlan:
+    """The plan for these offsets, built on first use and kept on the
+    ``cu_seqlens_q`` tensor object itself (so it lives exactly as long as
+    that tensor); an in-place change of either offsets tensor (its
+    ``_version``) or other totals / heads / causality build a new one."""
+    key = (cu_seqlens_q._version, cu_seqlens_k._version, int(total_q), int(total_k), int(hq) // int(hkv), int(hkv),
+           bool(causal), str(device))
+    cache = getattr(cu_seqlens_q, _PLAN_ATTR, None)
+    if cache is not None:
+        hit = cache.get(key)
+        if hit is not None and hit[0]() is cu_seqlens_k:
+            return hit[1]
+    plan = build_attn_plan(cu_seqlens_q, cu_seqlens_k, total_q, total_k, hq, hkv, causal, device)
+    try:
+        new = dict(cache) if cache is not None else {}
+        if len(new) >= 4:
+            new.clear()
+        new[key] = (weakref.ref(cu_seqlens_k), plan)
+        setattr(cu_seqlens_q, _PLAN_ATTR, new)
+    except (AttributeError, TypeError, RuntimeError):  # tensors that refuse attributes are simply not cached
+        pass
+    return plan
+
+
+def _resolve_plan(plan, cu_seqlens_q, cu_seqlens_k, total_q, total_k, hq, hkv, causal, device) -> AttnPlan:
+    if plan is None:
+        return cached_attn_plan(cu_seqlens_q, cu_seqlens_k, total_q, total_k, hq, hkv, causal, device)
+    if not plan.matches(plan.batch, total_q, total_k, hq, hkv, causal) or plan.buf.device != device:
+        raise ValueError("the attention plan was built for other sequences, heads or causality")
+    return plan
+
+
 # --------------------------------------------------------------------------- raw operators
 def varlen_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
                     cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
-                    causal: bool) -> tuple[torch.Tensor, torch.Tensor]:
-    """Returns ``(out [total_q, hq, d] bf16, lse [hq, total_q] fp32, natural log)``."""
+                    causal: bool, plan: AttnPlan | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Returns ``(out [total_q, hq, d] bf16, lse [hq, total_q] fp32, natural log)``.
+    ``plan`` None: the cached plan of ``cu_seqlens_q`` (built on first use)."""
     hq, hkv, d = _check_common(q, k, v)
     total_q, total_k = q.shape[0], k.shape[0]
-    cu_q = _device_cu(cu_seqlens_q, q.device, total_q, "cu_seqlens_q")
-    cu_k = _device_cu(cu_seqlens_k, q.device, total_k, "cu_seqlens_k")
-    if cu_q.numel() != cu_k.numel():
-        raise ValueError("cu_seqlens_q and cu_seqlens_k must describe the same number of sequences")
-    batch = cu_q.numel() - 1
+    pl = _resolve_plan(plan, cu_seqlens_q, cu_seqlens_k, total_q, total_k, hq, hkv, causal, q.device)
     out = torch.empty((total_q, hq, d), dtype=q.dtype, device=q.device)
     lse = torch.empty((hq, total_q), dtype=torch.float32, device=q.device)
     L = _lib.lib()
-    ws_bytes = L.siq_attn_fwd_workspace_bytes(batch, total_q, total_k, hq, hkv, d)
-    ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=q.device)
     strides = _lib.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
                                 out.stride(0), out.stride(1)])
-    rc = L.siq_attn_varlen_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
-                               cu_q.data_ptr(), cu_k.data_ptr(), batch, int(max_seqlen_q), int(max_seqlen_k),
-                               total_q, total_k, hq, hkv, d, strides, float(softmax_scale), int(bool(causal)),
-                               ws.data_ptr(), ws.numel(), _stream(q.device))
-    _lib.check(rc, "siq_attn_varlen_fwd")
+    rc = L.siq_attn_varlen_fwd_plan(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                    pl.batch, total_q, total_k, hq, hkv, d, strides, float(softmax_scale),
+                                    int(bool(causal)), pl.buf.data_ptr(), pl.buf.numel(), _stream(q.device))
+    _lib.check(rc, "siq_attn_varlen_fwd_plan")
     return out, lse
 
 
 def varlen_attn_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
                     lse: torch.Tensor, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
-                    max_seqlen_k: int, softmax_scale: float,
-                    causal: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                    max_seqlen_k: int, softmax_scale: float, causal: bool,
+                    plan: AttnPlan | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Returns ``(dq, dk, dv)``, bitwise deterministic."""
     hq, hkv, d = _check_common(q, k, v)
     total_q, total_k = q.shape[0], k.shape[0]
@@ -152,24 +235,21 @@ def varlen_attn_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: tor
         raise ValueError("out / dout must have total_q rows")
     if lse.shape != (hq, total_q) or lse.dtype != torch.float32 or not lse.is_contiguous():
         raise ValueError(f"lse must be a contiguous fp32 [{hq}, {total_q}] tensor")
-    cu_q = _device_cu(cu_seqlens_q, q.device, total_q, "cu_seqlens_q")
-    cu_k = _device_cu(cu_seqlens_k, q.device, total_k, "cu_seqlens_k")
-    batch = cu_q.numel() - 1
+    pl = _resolve_plan(plan, cu_seqlens_q, cu_seqlens_k, total_q, total_k, hq, hkv, causal, q.device)
     dq = torch.empty((total_q, hq, d), dtype=q.dtype, device=q.device)
     dk = torch.empty((total_k, hkv, d), dtype=q.dtype, device=q.device)
     dv = torch.empty((total_k, hkv, d), dtype=q.dtype, device=q.device)
     L = _lib.lib()
-    ws_bytes = L.siq_attn_bwd_workspace_bytes(batch, total_q, total_k, hq, hkv, d)
+    ws_bytes = L.siq_attn_bwd_plan_workspace_bytes(pl.batch, total_q, total_k, hq, hkv, d)
     ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=q.device)
     strides = _lib.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
                                 out.stride(0), out.stride(1), dout.stride(0), dout.stride(1), dq.stride(0),
                                 dq.stride(1), dk.stride(0), dk.stride(1), dv.stride(0), dv.stride(1)])
-    rc = L.siq_attn_varlen_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
-                               dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), cu_q.data_ptr(),
-                               cu_k.data_ptr(), batch, int(max_seqlen_q), int(max_seqlen_k), total_q, total_k, hq,
-                               hkv, d, strides, float(softmax_scale), int(bool(causal)), ws.data_ptr(), ws.numel(),
-                               _stream(q.device))
-    _lib.check(rc, "siq_attn_varlen_bwd")
+    rc = L.siq_attn_varlen_bwd_plan(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                    dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), pl.batch, total_q,
+                                    total_k, hq, hkv, d, strides, float(softmax_scale), int(bool(causal)),
+                                    pl.buf.data_ptr(), pl.buf.numel(), ws.data_ptr(), ws.numel(), _stream(q.device))
+    _lib.check(rc, "siq_attn_varlen_bwd_plan")
     return dq, dk, dv
 
 
@@ -177,19 +257,22 @@ class _VarlenAttnFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, scale, causal):
         q, k, v = (_ensure_token_major(t) for t in (q, k, v))
-        cu_q = _device_cu(cu_q, q.device, q.shape[0], "cu_seqlens_q")
-        cu_k = _device_cu(cu_k, q.device, k.shape[0], "cu_seqlens_k")
-        out, lse = varlen_attn_fwd(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal)
-        ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k)
+        hq, hkv = q.shape[1], k.shape[1]
+        plan = cached_attn_plan(cu_q, cu_k, q.shape[0], k.shape[0], hq, hkv, causal, q.device)
+        out, lse = varlen_attn_fwd(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, plan=plan)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.plan = plan
         ctx.args = (max_q, max_k, scale, causal)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q, k, v, out, lse, cu_q, cu_k = ctx.saved_tensors
+        q, k, v, out, lse = ctx.saved_tensors
         max_q, max_k, scale, causal = ctx.args
+        plan = ctx.plan
         dout = _ensure_token_major(dout)
-        dq, dk, dv = varlen_attn_bwd(dout, q, k, v, out, lse, cu_q, cu_k, max_q, max_k, scale, causal)
+        dq, dk, dv = varlen_attn_bwd(dout, q, k, v, out, lse, plan.cu_q, plan.cu_k, max_q, max_k, scale, causal,
+                                     plan=plan)
         return dq, dk, dv, None, None, None, None, None, None
 
 
@@ -222,17 +305,57 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu
 
 
 # --------------------------------------------------------------------------- transformers plug-in
+_DERIVED_ATTR = "_siq_attn_derived"
+
+
+def _cached_derived(t: torch.Tensor, tag: str, make):
+    """``make()``'s result kept on tensor ``t`` (keyed by ``tag`` and ``t``'s
+    version): the offsets derived from one batch's position_ids or padding
+    mask are computed -- with their one device-to-host read -- by the first
+    decoder layer and reused by the others, which receive the same tensor."""
+    key = (tag, t._version)
+    cache = getattr(t, _DERIVED_ATTR, None)
+    if cache is not None and key in cache:
+        return cache[key]
+    val = make()
+    try:
+        setattr(t, _DERIVED_ATTR, {key: val})
+    except (AttributeError, TypeError, RuntimeError):
+        pass
+    return val
+
+
 def _cu_from_position_ids(position_ids: torch.Tensor) -> tuple[torch.Tensor, int]:
     """Packed position_ids restart at 0 for each sequence (transformers
-    modeling_flash_attention_utils.py:458-495): offsets are where they do."""
-    pos = position_ids.reshape(-1)
-    starts = torch.nonzero(pos == 0, as_tuple=False).reshape(-1).to(torch.int32)
-    if starts.numel() == 0 or int(starts[0]) != 0:
-        starts = torch.cat([torch.zeros(1, dtype=torch.int32, device=pos.device), starts])
-    total = torch.tensor([pos.numel()], dtype=torch.int32, device=pos.device)
-    cu = torch.cat([starts, total])
-    max_len = int((cu[1:] - cu[:-1]).max().item())
-    return cu, max_len
+    modeling_flash_attention_utils.py:458-495): offsets are where they do.
+    Computed once per position_ids tensor (one host read of the longest
+    sequence), then reused."""
+
+    def make():
+        pos = position_ids.reshape(-1)
+        starts = torch.nonzero(pos == 0, as_tuple=False).reshape(-1).to(torch.int32)
+        if starts.numel() == 0 or int(starts[0]) != 0:
+            starts = torch.cat([torch.zeros(1, dtype=torch.int32, device=pos.device), starts])
+        total = torch.tensor([pos.numel()], dtype=torch.int32, device=pos.device)
+        cu = torch.cat([starts, total])
+        max_len = int((cu[1:] - cu[:-1]).max().item())
+        return cu, max_len
+
+    return _cached_derived(position_ids, "pos", make)
+
+
+def _unpad_from_mask(mask2d: torch.Tensor, s_k: int) -> tuple[torch.Tensor, torch.Tensor, int]:
+    """(cu_seqlens, kept token indices, longest row) of a 2-D padding mask,
+    computed once per mask tensor."""
+
+    def make():
+        mask = mask2d[:, -s_k:].to(torch.bool)
+        seqlens = mask.sum(dim=-1, dtype=torch.int32)
+        cu = torch.nn.functional.pad(torch.cumsum(seqlens, 0, dtype=torch.int32), (1, 0))
+        idx = torch.nonzero(mask.reshape(-1), as_tuple=False).reshape(-1)
+        return cu, idx, int(seqlens.max().item())
+
+    return _cached_derived(mask2d, f"mask{s_k}", make)
 
 
 def siq_varlen_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: torch.Tensor,
@@ -277,11 +400,7 @@ def siq_varlen_attention_forward(module: torch.nn.Module, query: torch.Tensor, k
                                      softmax_scale=scaling, causal=is_causal)
         out = out.reshape(bsz, s_q, hq, d)
     elif attention_mask is not None and attention_mask.dim() == 2:
-        mask = attention_mask[:, -s_k:].to(torch.bool)
-        seqlens = mask.sum(dim=-1, dtype=torch.int32)
-        cu = torch.nn.functional.pad(torch.cumsum(seqlens, 0, dtype=torch.int32), (1, 0))
-        idx = torch.nonzero(mask.reshape(-1), as_tuple=False).reshape(-1)
-        maxlen = int(seqlens.max().item())
+        cu, idx, maxlen = _unpad_from_mask(attention_mask, s_k)
         if s_q != s_k:
             raise ValueError("padded (unpacked) inputs need equal query and key lengths")
         qu = q.reshape(-1, hq, d).index_select(0, idx)
@@ -337,6 +456,9 @@ def attention_flops(cu_seqlens: torch.Tensor, hq: int, d: int, causal: bool, bac
 
 __all__ = [
     "ATTN_IMPLEMENTATION",
+    "AttnPlan",
+    "build_attn_plan",
+    "cached_attn_plan",
     "attention_flops",
     "flash_attn_varlen_func",
     "register",

@@ -6,43 +6,46 @@ Replaces, in the reference path, ``logits = lm_head(h)``
 loss/loss_utils.py:32-71: fp32 upcast, ``F.cross_entropy`` with
 ``ignore_index=-100``, ``"mean"`` or ``"sum" / num_items_in_batch``) and
 their autograd backward, by one call of ``siq_flce_fwd_bwd`` that never
-holds more than one token chunk of (exp-normalised) logits.
+holds more than one token chunk of (exp-normalised) logits, bounded at
+``DEFAULT_E_BUDGET_BYTES``.
 
 The forward computes the loss and both gradients at once; the backward only
 rescales them by the upstream gradient (a device scalar, no host sync).
+Without gradients (evaluation) the loss-only ``siq_flce_loss`` runs.
 """
 
 from __future__ import annotations
+
+import threading
 
 import torch
 
 from . import _lib
 
-# Token rows per logits chunk.  One chunk's softmax numerators are chunk x vocab
-# bf16 (5.0 GB at 16384 x 151936); a whole 16384-token batch in one chunk runs
-# 3% faster on MI355X than two chunks of 8192 and needs no fp32 dW accumulator.
-DEFAULT_CHUNK_TOKENS = 16384
 IGNORE_INDEX = -100
+# Bound on the one logits-sized buffer, a token chunk's softmax numerators
+# (chunk x vocab bf16).  At vocab 151,936 this is 6,912 rows (2.1 GB, against
+# 5.0 GB for the bf16 logits of a 16,384-token batch and 10 GB for the fp32
+# logits the reference's ForCausalLMLoss upcasts to).
+DEFAULT_E_BUDGET_BYTES = 2 << 30
 
 
-def flce_workspace_bytes(n: int, hdim: int, vocab: int, chunk_tokens: int, need_dweight: bool) -> int:
-    return int(_lib.lib().siq_flce_workspace_bytes(n, hdim, vocab, chunk_tokens, int(bool(need_dweight))))
+def default_chunk_tokens(vocab: int, budget_bytes: int = DEFAULT_E_BUDGET_BYTES) -> int:
+    """Token rows per logits chunk: the most 256-row tiles whose numerators
+    (rows x vocab bf16) fit in ``budget_bytes`` (at least one tile)."""
+    rows = budget_bytes // (2 * max(int(vocab), 1))
+    return max(256, (rows // 256) * 256)
 
 
-def flce_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor, ignore_index: int = IGNORE_INDEX,
-                 divisor: torch.Tensor | None = None, need_dweight: bool = True,
-                 chunk_tokens: int = DEFAULT_CHUNK_TOKENS):
-    """Raw operator.
+def flce_workspace_bytes(n: int, hdim: int, vocab: int, chunk_tokens: int | None, need_dweight: bool) -> int:
+    chunk = default_chunk_tokens(vocab) if chunk_tokens is None else int(chunk_tokens)
+    return int(_lib.lib().siq_flce_workspace_bytes(n, hdim, vocab, chunk, int(bool(need_dweight))))
 
-    ``hidden [n, hdim]`` bf16, ``weight [vocab, hdim]`` bf16, ``labels [n]`` int64
-    (already shifted).  ``divisor`` None -> mean over valid rows; else a
-    device scalar: loss = sum / divisor.  Returns
-    ``(loss fp32 [], count int64 [], bad_labels int64 [], dhidden, dweight | None)``.
-    """
+
+def _check_operands(hidden, weight, labels):
     if hidden.dim() != 2 or weight.dim() != 2:
         raise ValueError("hidden must be [n, hdim] and weight [vocab, hdim]")
     n, hdim = hidden.shape
-    vocab = weight.shape[0]
     if weight.shape[1] != hdim:
         raise ValueError(f"weight hdim {weight.shape[1]} != hidden hdim {hdim}")
     for name, t in (("hidden", hidden), ("weight", weight)):
@@ -54,7 +57,31 @@ def flce_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tenso
         raise ValueError(f"labels must be [n] = [{n}], got {tuple(labels.shape)}")
     if labels.dtype != torch.int64:
         raise ValueError(f"labels must be int64, got {labels.dtype}")
-    if chunk_tokens <= 0:
+
+
+def _divisor(divisor, dev):
+    if divisor is None:
+        return None, 0, None
+    divisor = divisor.to(device=dev, dtype=torch.float32).reshape(())
+    return divisor, 1, divisor.data_ptr()
+
+
+def flce_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor, ignore_index: int = IGNORE_INDEX,
+                 divisor: torch.Tensor | None = None, need_dweight: bool = True,
+                 chunk_tokens: int | None = None):
+    """Raw operator.
+
+    ``hidden [n, hdim]`` bf16, ``weight [vocab, hdim]`` bf16, ``labels [n]`` int64
+    (already shifted).  ``divisor`` None -> mean over valid rows; else a
+    device scalar: loss = sum / divisor.  ``chunk_tokens`` None -> the
+    default bound (``default_chunk_tokens``).  Returns
+    ``(loss fp32 [], count int64 [], bad_labels int64 [], dhidden, dweight | None)``.
+    """
+    _check_operands(hidden, weight, labels)
+    n, hdim = hidden.shape
+    vocab = weight.shape[0]
+    chunk = default_chunk_tokens(vocab) if chunk_tokens is None else int(chunk_tokens)
+    if chunk <= 0:
         raise ValueError("chunk_tokens must be positive")
     dev = hidden.device
     hidden = hidden.contiguous()
@@ -65,38 +92,120 @@ def flce_fwd_bwd(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tenso
     bad = torch.empty((), dtype=torch.int64, device=dev)
     dh = torch.empty_like(hidden)
     dw = torch.empty_like(weight) if need_dweight else None
-    reduction = 0
-    div_ptr = None
-    if divisor is not None:
-        divisor = divisor.to(device=dev, dtype=torch.float32).reshape(())
-        reduction = 1
-        div_ptr = divisor.data_ptr()
+    divisor, reduction, div_ptr = _divisor(divisor, dev)
     L = _lib.lib()
-    ws_bytes = L.siq_flce_workspace_bytes(n, hdim, vocab, chunk_tokens, int(need_dweight))
+    ws_bytes = L.siq_flce_workspace_bytes(n, hdim, vocab, chunk, int(need_dweight))
     ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=dev)
     rc = L.siq_flce_fwd_bwd(hidden.data_ptr(), weight.data_ptr(), labels.data_ptr(), n, hdim, vocab,
                             int(ignore_index), reduction, div_ptr, loss.data_ptr(), count.data_ptr(), bad.data_ptr(),
-                            dh.data_ptr(), dw.data_ptr() if dw is not None else None, int(chunk_tokens),
+                            dh.data_ptr(), dw.data_ptr() if dw is not None else None, chunk,
                             ws.data_ptr(), ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
     _lib.check(rc, "siq_flce_fwd_bwd")
     return loss, count, bad, dh, dw
 
 
-def _scale_(t: torch.Tensor | None, g: torch.Tensor) -> None:
-    if t is None:
+def flce_loss(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor, ignore_index: int = IGNORE_INDEX,
+              divisor: torch.Tensor | None = None):
+    """Loss only (``siq_flce_loss``): the logits GEMM and the chunked
+    logsumexp, no gradient work.  Returns ``(loss, count, bad_labels)``,
+    bitwise those of ``flce_fwd_bwd`` on the same inputs."""
+    _check_operands(hidden, weight, labels)
+    n, hdim = hidden.shape
+    vocab = weight.shape[0]
+    dev = hidden.device
+    hidden = hidden.contiguous()
+    weight = weight.contiguous()
+    labels = labels.to(dev).contiguous()
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    count = torch.empty((), dtype=torch.int64, device=dev)
+    bad = torch.empty((), dtype=torch.int64, device=dev)
+    divisor, reduction, div_ptr = _divisor(divisor, dev)
+    L = _lib.lib()
+    ws_bytes = L.siq_flce_loss_workspace_bytes(n, hdim, vocab)
+    ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=dev)
+    rc = L.siq_flce_loss(hidden.data_ptr(), weight.data_ptr(), labels.data_ptr(), n, hdim, vocab, int(ignore_index),
+                         reduction, div_ptr, loss.data_ptr(), count.data_ptr(), bad.data_ptr(), ws.data_ptr(),
+                         ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
+    _lib.check(rc, "siq_flce_loss")
+    return loss, count, bad
+
+
+class LabelError(ValueError):
+    """A label outside [0, vocab) that is not ignore_index (F.cross_entropy
+    rejects those too)."""
+
+
+# Out-of-range labels are counted on the device.  Reading that count at once
+# would stall the host on every step, so by default it is copied to pinned
+# host memory without blocking and checked when the copy has landed: at the
+# next call, or when check_pending_labels() is called.  validate="sync" reads it
+# at once (one device-to-host sync), validate=False never checks.
+_PENDING: list = []
+_PENDING_LOCK = threading.Lock()
+
+
+def _raise_bad(nbad: int, vocab: int, ignore_index: int) -> None:
+    raise LabelError(f"fused cross-entropy: {nbad} label(s) outside [0, {vocab}) that are not ignore_index "
+                     f"({ignore_index}); F.cross_entropy rejects such targets")
+
+
+def check_pending_labels(block: bool = False) -> None:
+    """Raises LabelError for any earlier call whose bad-label count has landed
+    and is non-zero (all of them when ``block``)."""
+    with _PENDING_LOCK:
+        keep = []
+        found = None
+        for ev, host, vocab, ign in _PENDING:
+            if block:
+                ev.synchronize()
+            if ev.query():
+                if int(host) > 0 and found is None:
+                    found = (int(host), vocab, ign)
+            else:
+                keep.append((ev, host, vocab, ign))
+        _PENDING[:] = keep
+    if found is not None:
+        _raise_bad(*found)
+
+
+def _track_bad(bad: torch.Tensor, vocab: int, ignore_index: int, validate) -> None:
+    if validate is False or validate is None:
         return
-    rc = _lib.lib().siq_scale_bf16_inplace(t.data_ptr(), t.numel(), g.data_ptr(),
-                                           torch.cuda.current_stream(t.device).cuda_stream)
-    _lib.check(rc, "siq_scale_bf16_inplace")
+    if validate == "sync":
+        nbad = int(bad)
+        if nbad > 0:
+            _raise_bad(nbad, vocab, ignore_index)
+        return
+    check_pending_labels()
+    host = torch.empty((), dtype=torch.int64, pin_memory=True)
+    host.copy_(bad, non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record(torch.cuda.current_stream(bad.device))
+    with _PENDING_LOCK:
+        _PENDING.append((ev, host, vocab, ignore_index))
+
+
+def _scaled(t: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    """t * g as a new bf16 tensor (the saved gradients stay untouched, so a
+    second backward through a retained graph sees them unscaled)."""
+    out = torch.empty_like(t)
+    rc = _lib.lib().siq_scale_bf16(t.data_ptr(), out.data_ptr(), t.numel(), g.data_ptr(),
+                                   torch.cuda.current_stream(t.device).cuda_stream)
+    _lib.check(rc, "siq_scale_bf16")
+    return out
 
 
 class _FusedLinearCE(torch.autograd.Function):
+    """Loss forward; its backward returns the gradients the forward already
+    computed, times the upstream gradient."""
+
     @staticmethod
-    def forward(ctx, hidden, weight, labels, ignore_index, divisor, chunk_tokens):
+    def forward(ctx, hidden, weight, labels, ignore_index, divisor, chunk_tokens, validate):
         shape = hidden.shape
         h2 = hidden.reshape(-1, shape[-1])
-        loss, _, _, dh, dw = flce_fwd_bwd(h2, weight, labels.reshape(-1), ignore_index, divisor,
-                                          need_dweight=weight.requires_grad, chunk_tokens=chunk_tokens)
+        loss, _, bad, dh, dw = flce_fwd_bwd(h2, weight, labels.reshape(-1), ignore_index, divisor,
+                                            need_dweight=weight.requires_grad, chunk_tokens=chunk_tokens)
+        _track_bad(bad, weight.shape[0], ignore_index, validate)
         ctx.shape = shape
         ctx.save_for_backward(dh, dw if dw is not None else torch.empty(0, device=hidden.device))
         ctx.has_dw = dw is not None
@@ -106,21 +215,27 @@ class _FusedLinearCE(torch.autograd.Function):
     def backward(ctx, grad_loss):
         dh, dw = ctx.saved_tensors
         g = grad_loss.detach().to(torch.float32).reshape(()).contiguous()
-        _scale_(dh, g)
-        if ctx.has_dw:
-            _scale_(dw, g)
-        return dh.reshape(ctx.shape), (dw if ctx.has_dw else None), None, None, None, None
+        gh = _scaled(dh, g).reshape(ctx.shape) if ctx.needs_input_grad[0] else None
+        gw = _scaled(dw, g) if ctx.has_dw and ctx.needs_input_grad[1] else None
+        return gh, gw, None, None, None, None, None
 
 
 def fused_linear_cross_entropy(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
                                ignore_index: int = IGNORE_INDEX, num_items_in_batch=None,
-                               chunk_tokens: int = DEFAULT_CHUNK_TOKENS) -> torch.Tensor:
+                               chunk_tokens: int | None = None, validate="lazy") -> torch.Tensor:
     """``F.cross_entropy(hidden @ weight.T, labels, ignore_index)`` without logits.
 
     ``labels`` are the already-shifted targets (same shape as ``hidden[..., 0]``).
     With ``num_items_in_batch`` the loss is ``sum / num_items_in_batch`` as in
     ``fixed_cross_entropy``; otherwise the mean over non-ignored rows (NaN if
     every row is ignored, like ``F.cross_entropy``).
+
+    When no gradient can flow (grad mode off, or neither ``hidden`` nor
+    ``weight`` requires grad) only the loss is computed (``flce_loss``).
+    Labels outside ``[0, vocab)`` other than ``ignore_index`` raise
+    ``LabelError``: ``validate="lazy"`` (default) without a host sync, at the
+    next call or ``check_pending_labels()``; ``"sync"`` at once; ``False``
+    never.
     """
     divisor = None
     if num_items_in_batch is not None:
@@ -130,7 +245,11 @@ def fused_linear_cross_entropy(hidden: torch.Tensor, weight: torch.Tensor, label
             divisor = torch.tensor(float(num_items_in_batch), dtype=torch.float32, device=hidden.device)
     h = hidden if hidden.dtype == torch.bfloat16 else hidden.to(torch.bfloat16)
     w = weight if weight.dtype == torch.bfloat16 else weight.to(torch.bfloat16)
-    return _FusedLinearCE.apply(h, w, labels, int(ignore_index), divisor, int(chunk_tokens))
+    if not torch.is_grad_enabled() or not (h.requires_grad or w.requires_grad):
+        loss, _, bad = flce_loss(h.reshape(-1, h.shape[-1]), w, labels.reshape(-1), int(ignore_index), divisor)
+        _track_bad(bad, w.shape[0], int(ignore_index), validate)
+        return loss
+    return _FusedLinearCE.apply(h, w, labels, int(ignore_index), divisor, chunk_tokens, validate)
 
 
 def shift_labels(labels: torch.Tensor, ignore_index: int = IGNORE_INDEX) -> torch.Tensor:
@@ -145,10 +264,14 @@ def ce_flops(n: int, hdim: int, vocab: int) -> float:
 
 
 __all__ = [
-    "DEFAULT_CHUNK_TOKENS",
+    "DEFAULT_E_BUDGET_BYTES",
     "IGNORE_INDEX",
+    "LabelError",
     "ce_flops",
+    "check_pending_labels",
+    "default_chunk_tokens",
     "flce_fwd_bwd",
+    "flce_loss",
     "flce_workspace_bytes",
     "fused_linear_cross_entropy",
     "shift_labels",

@@ -59,6 +59,23 @@ __device__ __forceinline__ int xcd_order(int b, int n, int G) {
   return ((k / G) * kXcds + x) * G + (k % G);
 }
 
+// Header of an attention plan (the schedule of one packed batch, reusable
+// by every layer's forward and backward).  The scheduler writes it; each
+// attention kernel compares it with its own arguments before using the plan
+// and, on a mismatch, leaves its outputs alone and flags kStatusMismatch
+// (a plan built for other sequences or heads could otherwise send a kernel
+// outside its tensors).  status_q / status_kv: bits set by the scheduler's two
+// blocks (kStatusOverflow: a work list or the split slots would not hold the
+// schedule -- impossible by the bounds below, kept as a tripwire).
+constexpr int kPlanMagic = 0x51504c4e;  // "QPLN"
+constexpr int kStatusOverflow = 1;
+constexpr int kStatusMismatch = 2;
+struct PlanHeader {
+  int64_t total_q, total_k;
+  int magic, batch, n_rep, hkv, causal, has_kv;
+  int status_q, status_kv, status_use, pad;
+};
+
 struct AttnParams {
   const bf16* q;
   const bf16* k;
@@ -78,6 +95,7 @@ struct AttnParams {
   float* dkv_part;           // [kSplitSlots][2][kBwdBN][D] fp32 partial dK / dV of split tiles
   const SplitTile* splits;   // [kMaxSplitTiles] split tiles
   const int* nsplit;         // number of split tiles
+  PlanHeader* plan;          // the plan these lists belong to
   int batch, hq, hkv, n_rep;
   int64_t q_tok, q_head, k_tok, k_head, v_tok, v_head, o_tok, o_head;
   int64_t do_tok, do_head, dq_tok, dq_head, dk_tok, dk_head, dv_tok, dv_head;
@@ -95,9 +113,20 @@ inline int64_t kv_item_cap(int64_t total_k, int batch) {
   return tile_cap(total_k, batch, kBwdBN) + 2 * kSplitTarget + 1;
 }
 
+// True when the plan was built for these arguments (read by one lane; the
+// caller returns on false).  A mismatch is recorded in the plan's status_use.
+__device__ __forceinline__ bool plan_matches(const AttnParams& p, bool causal, bool need_kv) {
+  const PlanHeader h = *p.plan;
+  const bool ok = h.magic == kPlanMagic && h.total_q == p.total_q && h.total_k == p.total_k &&
+                  h.batch == p.batch && h.n_rep == p.n_rep && h.hkv == p.hkv && h.causal == (causal ? 1 : 0) &&
+                  (!need_kv || h.has_kv);
+  if (!ok && threadIdx.x == 0) atomicOr(&p.plan->status_use, kStatusMismatch);
+  return ok;
+}
+
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,
-                           int causal, int n_rep, int hkv, SeqInfo* seq, QTile* qtiles, int qrows, int qcap,
-                           KvItem* kvitems, int kvcap, int* seqbuf, SplitTile* splits, int* nsplit,
+                           int causal, int n_rep, int hkv, PlanHeader* plan, SeqInfo* seq, QTile* qtiles, int qrows,
+                           int qcap, KvItem* kvitems, int kvcap, int* seqbuf, SplitTile* splits, int* nsplit,
                            hipStream_t stream);
 hipError_t launch_attn_fwd(const AttnParams& p, int d, int causal, int qcap, hipStream_t stream);
 hipError_t launch_attn_bwd(const AttnParams& p, int d, int causal, int qcap, int kvcap, hipStream_t stream);

@@ -75,7 +75,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
   // fetch b alone, wait for it, then fetch the rest)
   asm volatile("" : : "s"(it.s.q_start), "s"(it.s.q_len), "s"(it.s.k_start), "s"(it.s.k_len), "s"(it.t), "s"(it.s0),
                "s"(it.s1));
-  if (it.b < 0) return;
+  if (!plan_matches(p, CAUSAL, true) || it.b < 0) return;
   const SeqInfo si = it.s;
   const int k0 = it.t * BN;
   const int kb = k0 + 32 * kq;  // first kv row of this wave
@@ -332,6 +332,7 @@ template <int D>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_sum_kernel(const AttnParams p) {
   using S = DkvSum<D>;
   constexpr int BN = kBwdBN;
+  if (!plan_matches(p, p.plan->causal != 0, true)) return;
   const int units = *p.nsplit * S::NCH;
   for (int unit = blockIdx.x; unit < units; unit += gridDim.x) {
   const int tile = unit / S::NCH, ch = unit % S::NCH;
@@ -395,7 +396,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
   // every field loaded before the idle test (the compiler would otherwise
   // fetch b alone, wait for it, then fetch the rest)
   asm volatile("" : : "s"(tl.s.q_start), "s"(tl.s.q_len), "s"(tl.s.k_start), "s"(tl.s.k_len), "s"(tl.t));
-  if (tl.b < 0) return;
+  if (!plan_matches(p, CAUSAL, false) || tl.b < 0) return;
   const SeqInfo si = tl.s;
   const int q0 = tl.t * BM;
   const int off = si.k_len - si.q_len;

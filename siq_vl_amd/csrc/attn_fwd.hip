@@ -59,7 +59,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   // every field loaded before the idle test (the compiler would otherwise
   // fetch b alone, wait for it, then fetch the rest)
   asm volatile("" : : "s"(tl.s.q_start), "s"(tl.s.q_len), "s"(tl.s.k_start), "s"(tl.s.k_len), "s"(tl.t));
-  if (tl.b < 0) return;
+  if (!plan_matches(p, CAUSAL, false) || tl.b < 0) return;
   const SeqInfo si = tl.s;
   const int q0 = tl.t * BM;
   const int off = si.k_len - si.q_len;

@@ -11,6 +11,7 @@
 #include "../../include/siq_kernels.h"
 #include "attn.h"
 #include "flce.h"
+#include "probe.h"
 #include "proj.h"
 #include "rope.h"
 #include "splice.h"
@@ -38,16 +39,21 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-struct AttnLayout {
-  size_t seq, qtiles, kvitems, seqbuf, splits, nsplit, part, delta, lse2, total;
+// An attention plan: header, per-sequence extents, the q-tile list (forward,
+// dQ) and the dK/dV work items with their split tiles.  It depends on the
+// sequences, the head counts and causality, not on the tensors.
+struct PlanLayout {
+  size_t header, seq, qtiles, kvitems, seqbuf, splits, nsplit, total;
   int qcap, kvcap;
 };
 
-AttnLayout attn_layout(int batch, int64_t total_q, int64_t total_k, int hq, int d, bool bwd) {
-  AttnLayout L{};
+PlanLayout plan_layout(int batch, int64_t total_q, int64_t total_k, bool kv) {
+  PlanLayout L{};
   L.qcap = (int)siq::tile_cap(total_q, batch, siq::kFwdBM);
-  L.kvcap = bwd ? (int)siq::kv_item_cap(total_k, batch) : 0;
+  L.kvcap = kv ? (int)siq::kv_item_cap(total_k, batch) : 0;
   size_t off = 0;
+  L.header = off;
+  off += align256(sizeof(siq::PlanHeader));
   L.seq = off;
   off += align256(sizeof(siq::SeqInfo) * (size_t)(batch > 0 ? batch : 1));
   L.qtiles = off;
@@ -55,23 +61,49 @@ AttnLayout attn_layout(int batch, int64_t total_q, int64_t total_k, int hq, int 
   L.kvitems = off;
   off += align256(sizeof(siq::KvItem) * (size_t)L.kvcap);
   L.seqbuf = off;
-  if (bwd) off += align256(sizeof(int) * ((size_t)(batch > 0 ? batch : 1) + 1));
+  if (kv) off += align256(sizeof(int) * ((size_t)(batch > 0 ? batch : 1) + 1));
   L.splits = off;
-  if (bwd) off += align256(sizeof(siq::SplitTile) * (size_t)siq::kMaxSplitTiles);
+  if (kv) off += align256(sizeof(siq::SplitTile) * (size_t)siq::kMaxSplitTiles);
   L.nsplit = off;
-  if (bwd) off += 256;
-  L.part = off;
-  if (bwd) off += align256(sizeof(float) * (size_t)siq::kSplitSlots * 2 * siq::kBwdBN * (size_t)d);
-  L.delta = off;
-  if (bwd) off += align256(sizeof(float) * (size_t)hq * (size_t)total_q);
-  L.lse2 = off;
-  if (bwd) off += align256(sizeof(float) * (size_t)hq * (size_t)total_q);
+  if (kv) off += 256;
   L.total = off;
   return L;
 }
 
+// The backward's own scratch beyond the plan: split-tile partial sums,
+// Delta = rowsum(dO o O) and LSE * log2(e).
+struct BwdLayout {
+  size_t part, delta, lse2, total;
+};
+
+BwdLayout bwd_layout(int64_t total_q, int hq, int d) {
+  BwdLayout L{};
+  size_t off = 0;
+  L.part = off;
+  off += align256(sizeof(float) * (size_t)siq::kSplitSlots * 2 * siq::kBwdBN * (size_t)d);
+  L.delta = off;
+  off += align256(sizeof(float) * (size_t)hq * (size_t)total_q);
+  L.lse2 = off;
+  off += align256(sizeof(float) * (size_t)hq * (size_t)total_q);
+  L.total = off;
+  return L;
+}
+
+// Builds the plan at `base` (laid out by L) on `stream`.
+hipError_t build_plan(char* base, const PlanLayout& L, const int32_t* cu_q, const int32_t* cu_k, int batch,
+                      int64_t total_q, int64_t total_k, int hq, int hkv, bool causal, bool kv, hipStream_t s) {
+  return siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal ? 1 : 0, hq / hkv, hkv,
+                              reinterpret_cast<siq::PlanHeader*>(base + L.header),
+                              reinterpret_cast<siq::SeqInfo*>(base + L.seq),
+                              reinterpret_cast<siq::QTile*>(base + L.qtiles), siq::kFwdBM, L.qcap,
+                              kv ? reinterpret_cast<siq::KvItem*>(base + L.kvitems) : nullptr, L.kvcap,
+                              kv ? reinterpret_cast<int*>(base + L.seqbuf) : nullptr,
+                              kv ? reinterpret_cast<siq::SplitTile*>(base + L.splits) : nullptr,
+                              kv ? reinterpret_cast<int*>(base + L.nsplit) : nullptr, s);
+}
+
 int check_attn_common(int batch, int max_q, int max_k, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
-                      float scale, const void* cu_q, const void* cu_k) {
+                      float scale) {
   if (batch < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "batch must be >= 0 (got %d)", batch);
   if (total_q < 0 || total_k < 0 || total_q >= (int64_t(1) << 31) || total_k >= (int64_t(1) << 31))
     return fail(SIQ_ERR_INVALID_ARGUMENT, "total_q/total_k must be in [0, 2^31) (got %lld, %lld)",
@@ -82,6 +114,10 @@ int check_attn_common(int batch, int max_q, int max_k, int64_t total_q, int64_t 
     return fail(SIQ_ERR_INVALID_ARGUMENT, "hq (%d) must be a multiple of hkv (%d) for GQA", hq, hkv);
   if (d != 64 && d != 128) return fail(SIQ_ERR_UNSUPPORTED, "head_dim %d unsupported (64 or 128)", d);
   if (!std::isfinite(scale)) return fail(SIQ_ERR_INVALID_ARGUMENT, "softmax_scale must be finite");
+  return SIQ_OK;
+}
+
+int check_cu(int batch, const void* cu_q, const void* cu_k) {
   if (batch > 0 && (cu_q == nullptr || cu_k == nullptr))
     return fail(SIQ_ERR_INVALID_ARGUMENT, "cu_seqlens_q / cu_seqlens_k must not be NULL");
   return SIQ_OK;
@@ -108,79 +144,90 @@ const char* siq_last_error(void) { return g_last_error.c_str(); }
 size_t siq_attn_fwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d) {
   (void)hkv;
   if (batch < 0 || total_q < 0 || total_k < 0 || hq <= 0 || d <= 0) return 0;
-  return attn_layout(batch, total_q, total_k, hq, d, false).total;
+  return plan_layout(batch, total_q, total_k, false).total;
 }
 
 size_t siq_attn_bwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d) {
   (void)hkv;
   if (batch < 0 || total_q < 0 || total_k < 0 || hq <= 0 || d <= 0) return 0;
-  return attn_layout(batch, total_q, total_k, hq, d, true).total;
+  return plan_layout(batch, total_q, total_k, true).total + bwd_layout(total_q, hq, d).total;
 }
 
-int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, float* lse, const int32_t* cu_q,
-                        const int32_t* cu_k, int batch, int max_q, int max_k, int64_t total_q, int64_t total_k,
-                        int hq, int hkv, int d, const int64_t* strides, float scale, int causal, void* ws,
-                        size_t ws_bytes, void* stream) {
-  int rc = check_attn_common(batch, max_q, max_k, total_q, total_k, hq, hkv, d, scale, cu_q, cu_k);
-  if (rc) return rc;
-  if (strides == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "strides must not be NULL");
-  const bool nq = total_q > 0, nk = total_k > 0;
-  if ((rc = check_tensor("q", q, strides + 0, nq)) || (rc = check_tensor("k", k, strides + 2, nk)) ||
-      (rc = check_tensor("v", v, strides + 4, nk)) || (rc = check_tensor("o", o, strides + 6, nq)))
-    return rc;
-  if (nq && (lse == nullptr || (reinterpret_cast<uintptr_t>(lse) & 3u)))
-    return fail(SIQ_ERR_ALIGNMENT, "lse must be a non-NULL 4-byte aligned fp32 pointer");
-  if (batch == 0 || total_q == 0) return ok();
-  const AttnLayout L = attn_layout(batch, total_q, total_k, hq, d, false);
-  if (ws == nullptr || ws_bytes < L.total || !aligned16(ws))
-    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", L.total, ws_bytes);
+size_t siq_attn_plan_bytes(int batch, int64_t total_q, int64_t total_k) {
+  if (batch < 0 || total_q < 0 || total_k < 0) return 0;
+  return plan_layout(batch, total_q, total_k, true).total;
+}
 
-  char* base = static_cast<char*>(ws);
-  siq::AttnParams p{};
-  p.q = static_cast<const siq::bf16*>(q);
-  p.k = static_cast<const siq::bf16*>(k);
-  p.v = static_cast<const siq::bf16*>(v);
-  p.out = static_cast<siq::bf16*>(o);
-  p.lse = lse;
+size_t siq_attn_bwd_plan_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d) {
+  (void)batch;
+  (void)total_k;
+  (void)hkv;
+  if (total_q < 0 || hq <= 0 || d <= 0) return 0;
+  return bwd_layout(total_q, hq, d).total;
+}
+
+int siq_attn_build_plan(const int32_t* cu_q, const int32_t* cu_k, int batch, int64_t total_q, int64_t total_k,
+                        int hq, int hkv, int causal, void* plan, size_t plan_bytes, void* stream) {
+  int rc = check_attn_common(batch, 0, 0, total_q, total_k, hq, hkv, 128, 1.f);
+  if (rc || (rc = check_cu(batch, cu_q, cu_k))) return rc;
+  const PlanLayout L = plan_layout(batch, total_q, total_k, true);
+  if (plan == nullptr || plan_bytes < L.total || !aligned16(plan))
+    return fail(SIQ_ERR_WORKSPACE, "plan needs %zu bytes (16-byte aligned), got %zu", L.total, plan_bytes);
+  const hipError_t e = build_plan(static_cast<char*>(plan), L, cu_q, cu_k, batch, total_q, total_k, hq, hkv,
+                                  causal != 0, true, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+}  // extern "C"
+
+namespace {
+
+// Fills the plan pointers of p from a plan laid out by L at base.
+void set_plan(siq::AttnParams& p, char* base, const PlanLayout& L) {
+  p.plan = reinterpret_cast<siq::PlanHeader*>(base + L.header);
   p.seq = reinterpret_cast<const siq::SeqInfo*>(base + L.seq);
   p.qtiles = reinterpret_cast<const siq::QTile*>(base + L.qtiles);
+  p.kvitems = reinterpret_cast<const siq::KvItem*>(base + L.kvitems);
+  p.splits = reinterpret_cast<const siq::SplitTile*>(base + L.splits);
+  p.nsplit = reinterpret_cast<const int*>(base + L.nsplit);
+}
+
+void set_common(siq::AttnParams& p, int batch, int64_t total_q, int64_t total_k, int hq, int hkv,
+                const int64_t* strides, int nstrides, float scale) {
   p.batch = batch;
   p.hq = hq;
   p.hkv = hkv;
   p.n_rep = hq / hkv;
-  p.q_tok = strides[0];
-  p.q_head = strides[1];
-  p.k_tok = strides[2];
-  p.k_head = strides[3];
-  p.v_tok = strides[4];
-  p.v_head = strides[5];
-  p.o_tok = strides[6];
-  p.o_head = strides[7];
+  int64_t* dst[16] = {&p.q_tok, &p.q_head, &p.k_tok, &p.k_head, &p.v_tok, &p.v_head, &p.o_tok, &p.o_head,
+                      &p.do_tok, &p.do_head, &p.dq_tok, &p.dq_head, &p.dk_tok, &p.dk_head, &p.dv_tok, &p.dv_head};
+  for (int i = 0; i < nstrides; ++i) *dst[i] = strides[i];
   p.lse_head = total_q;
   p.total_q = total_q;
   p.total_k = total_k;
   p.scale = scale;
   p.scale_log2 = scale * siq::kLog2e;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0, hq / hkv, hkv,
-                                      reinterpret_cast<siq::SeqInfo*>(base + L.seq),
-                                      reinterpret_cast<siq::QTile*>(base + L.qtiles), siq::kFwdBM, L.qcap, nullptr, 0,
-                                      nullptr, nullptr, nullptr, s);
-  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
-  e = siq::launch_attn_fwd(p, d, causal != 0, L.qcap, s);
-  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "attention forward launch failed: %s", hipGetErrorString(e));
-  return ok();
 }
 
-int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
-                        const void* dout, void* dq, void* dk, void* dv, const int32_t* cu_q, const int32_t* cu_k,
-                        int batch, int max_q, int max_k, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
-                        const int64_t* strides, float scale, int causal, void* ws, size_t ws_bytes,
-                        void* stream) {
-  int rc = check_attn_common(batch, max_q, max_k, total_q, total_k, hq, hkv, d, scale, cu_q, cu_k);
-  if (rc) return rc;
+int check_fwd_tensors(const void* q, const void* k, const void* v, void* o, float* lse, int64_t total_q,
+                      int64_t total_k, const int64_t* strides) {
   if (strides == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "strides must not be NULL");
   const bool nq = total_q > 0, nk = total_k > 0;
+  int rc;
+  if ((rc = check_tensor("q", q, strides + 0, nq)) || (rc = check_tensor("k", k, strides + 2, nk)) ||
+      (rc = check_tensor("v", v, strides + 4, nk)) || (rc = check_tensor("o", o, strides + 6, nq)))
+    return rc;
+  if (nq && (lse == nullptr || (reinterpret_cast<uintptr_t>(lse) & 3u)))
+    return fail(SIQ_ERR_ALIGNMENT, "lse must be a non-NULL 4-byte aligned fp32 pointer");
+  return SIQ_OK;
+}
+
+int check_bwd_tensors(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                      const void* dout, void* dq, void* dk, void* dv, int64_t total_q, int64_t total_k,
+                      const int64_t* strides) {
+  if (strides == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "strides must not be NULL");
+  const bool nq = total_q > 0, nk = total_k > 0;
+  int rc;
   if ((rc = check_tensor("q", q, strides + 0, nq)) || (rc = check_tensor("k", k, strides + 2, nk)) ||
       (rc = check_tensor("v", v, strides + 4, nk)) || (rc = check_tensor("o", o, strides + 6, nq)) ||
       (rc = check_tensor("dout", dout, strides + 8, nq)) || (rc = check_tensor("dq", dq, strides + 10, nq)) ||
@@ -188,12 +235,32 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
     return rc;
   if (nq && (lse == nullptr || (reinterpret_cast<uintptr_t>(lse) & 3u)))
     return fail(SIQ_ERR_ALIGNMENT, "lse must be a non-NULL 4-byte aligned fp32 pointer");
-  if (batch == 0 || (total_q == 0 && total_k == 0)) return ok();
-  const AttnLayout L = attn_layout(batch, total_q, total_k, hq, d, true);
-  if (ws == nullptr || ws_bytes < L.total || !aligned16(ws))
-    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", L.total, ws_bytes);
+  return SIQ_OK;
+}
 
-  char* base = static_cast<char*>(ws);
+// Forward over a built plan (at plan_base, laid out by L).
+int run_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int batch, int64_t total_q,
+            int64_t total_k, int hq, int hkv, int d, const int64_t* strides, float scale, int causal,
+            char* plan_base, const PlanLayout& L, hipStream_t s) {
+  siq::AttnParams p{};
+  p.q = static_cast<const siq::bf16*>(q);
+  p.k = static_cast<const siq::bf16*>(k);
+  p.v = static_cast<const siq::bf16*>(v);
+  p.out = static_cast<siq::bf16*>(o);
+  p.lse = lse;
+  set_plan(p, plan_base, L);
+  set_common(p, batch, total_q, total_k, hq, hkv, strides, 8, scale);
+  const hipError_t e = siq::launch_attn_fwd(p, d, causal != 0, L.qcap, s);
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "attention forward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+// Backward over a built plan and the backward's own scratch at ws.
+int run_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout, void* dq,
+            void* dk, void* dv, int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
+            const int64_t* strides, float scale, int causal, char* plan_base, const PlanLayout& L, char* ws,
+            hipStream_t s) {
+  const BwdLayout B = bwd_layout(total_q, hq, d);
   siq::AttnParams p{};
   p.q = static_cast<const siq::bf16*>(q);
   p.k = static_cast<const siq::bf16*>(k);
@@ -204,62 +271,112 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
   p.dq = static_cast<siq::bf16*>(dq);
   p.dk = static_cast<siq::bf16*>(dk);
   p.dv = static_cast<siq::bf16*>(dv);
-  p.delta = reinterpret_cast<float*>(base + L.delta);
-  p.lse2 = reinterpret_cast<float*>(base + L.lse2);
-  p.seq = reinterpret_cast<const siq::SeqInfo*>(base + L.seq);
-  p.qtiles = reinterpret_cast<const siq::QTile*>(base + L.qtiles);
-  p.kvitems = reinterpret_cast<const siq::KvItem*>(base + L.kvitems);
-  p.dkv_part = reinterpret_cast<float*>(base + L.part);
-  p.splits = reinterpret_cast<const siq::SplitTile*>(base + L.splits);
-  p.nsplit = reinterpret_cast<const int*>(base + L.nsplit);
-  p.batch = batch;
-  p.hq = hq;
-  p.hkv = hkv;
-  p.n_rep = hq / hkv;
-  p.q_tok = strides[0];
-  p.q_head = strides[1];
-  p.k_tok = strides[2];
-  p.k_head = strides[3];
-  p.v_tok = strides[4];
-  p.v_head = strides[5];
-  p.o_tok = strides[6];
-  p.o_head = strides[7];
-  p.do_tok = strides[8];
-  p.do_head = strides[9];
-  p.dq_tok = strides[10];
-  p.dq_head = strides[11];
-  p.dk_tok = strides[12];
-  p.dk_head = strides[13];
-  p.dv_tok = strides[14];
-  p.dv_head = strides[15];
-  p.lse_head = total_q;
-  p.total_q = total_q;
-  p.total_k = total_k;
-  p.scale = scale;
-  p.scale_log2 = scale * siq::kLog2e;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = siq::launch_schedule(cu_q, cu_k, batch, total_q, total_k, causal != 0, hq / hkv, hkv,
-                                      reinterpret_cast<siq::SeqInfo*>(base + L.seq),
-                                      reinterpret_cast<siq::QTile*>(base + L.qtiles), siq::kFwdBM, L.qcap,
-                                      reinterpret_cast<siq::KvItem*>(base + L.kvitems), L.kvcap,
-                                      reinterpret_cast<int*>(base + L.seqbuf),
-                                      reinterpret_cast<siq::SplitTile*>(base + L.splits),
-                                      reinterpret_cast<int*>(base + L.nsplit), s);
-  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
-  e = siq::launch_attn_bwd(p, d, causal != 0, L.qcap, L.kvcap, s);
+  p.delta = reinterpret_cast<float*>(ws + B.delta);
+  p.lse2 = reinterpret_cast<float*>(ws + B.lse2);
+  p.dkv_part = reinterpret_cast<float*>(ws + B.part);
+  set_plan(p, plan_base, L);
+  set_common(p, batch, total_q, total_k, hq, hkv, strides, 16, scale);
+  const hipError_t e = siq::launch_attn_bwd(p, d, causal != 0, L.qcap, L.kvcap, s);
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "attention backward launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 
-size_t siq_flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk_tokens, int need_dweight) {
-  if (n < 0 || hdim <= 0 || vocab <= 0) return 0;
-  return siq::flce_workspace_bytes(n, hdim, vocab, chunk_tokens, need_dweight != 0);
+}  // namespace
+
+extern "C" {
+
+int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, float* lse, const int32_t* cu_q,
+                        const int32_t* cu_k, int batch, int max_q, int max_k, int64_t total_q, int64_t total_k,
+                        int hq, int hkv, int d, const int64_t* strides, float scale, int causal, void* ws,
+                        size_t ws_bytes, void* stream) {
+  int rc = check_attn_common(batch, max_q, max_k, total_q, total_k, hq, hkv, d, scale);
+  if (rc || (rc = check_cu(batch, cu_q, cu_k))) return rc;
+  if ((rc = check_fwd_tensors(q, k, v, o, lse, total_q, total_k, strides))) return rc;
+  if (batch == 0 || total_q == 0) return ok();
+  const PlanLayout L = plan_layout(batch, total_q, total_k, false);
+  if (ws == nullptr || ws_bytes < L.total || !aligned16(ws))
+    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", L.total, ws_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* base = static_cast<char*>(ws);
+  const hipError_t e = build_plan(base, L, cu_q, cu_k, batch, total_q, total_k, hq, hkv, causal != 0, false, s);
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
+  return run_fwd(q, k, v, o, lse, batch, total_q, total_k, hq, hkv, d, strides, scale, causal, base, L, s);
 }
 
-int siq_flce_fwd_bwd(const void* hidden, const void* weight, const int64_t* labels, int64_t n, int64_t hdim,
-                     int64_t vocab, int64_t ignore_index, int reduction, const float* divisor, float* loss,
-                     int64_t* count, int64_t* bad_labels, void* dhidden, void* dweight, int64_t chunk_tokens,
-                     void* ws, size_t ws_bytes, void* stream) {
+int siq_attn_varlen_fwd_plan(const void* q, const void* k, const void* v, void* o, float* lse, int batch,
+                             int64_t total_q, int64_t total_k, int hq, int hkv, int d, const int64_t* strides,
+                             float scale, int causal, const void* plan, size_t plan_bytes, void* stream) {
+  int rc = check_attn_common(batch, 0, 0, total_q, total_k, hq, hkv, d, scale);
+  if (rc) return rc;
+  if ((rc = check_fwd_tensors(q, k, v, o, lse, total_q, total_k, strides))) return rc;
+  if (batch == 0 || total_q == 0) return ok();
+  const PlanLayout L = plan_layout(batch, total_q, total_k, true);
+  if (plan == nullptr || plan_bytes < L.total || !aligned16(plan))
+    return fail(SIQ_ERR_WORKSPACE, "plan needs %zu bytes (16-byte aligned), got %zu", L.total, plan_bytes);
+  return run_fwd(q, k, v, o, lse, batch, total_q, total_k, hq, hkv, d, strides, scale, causal,
+                 static_cast<char*>(const_cast<void*>(plan)), L, static_cast<hipStream_t>(stream));
+}
+
+int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                        const void* dout, void* dq, void* dk, void* dv, const int32_t* cu_q, const int32_t* cu_k,
+                        int batch, int max_q, int max_k, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
+                        const int64_t* strides, float scale, int causal, void* ws, size_t ws_bytes,
+                        void* stream) {
+  int rc = check_attn_common(batch, max_q, max_k, total_q, total_k, hq, hkv, d, scale);
+  if (rc || (rc = check_cu(batch, cu_q, cu_k))) return rc;
+  if ((rc = check_bwd_tensors(q, k, v, o, lse, dout, dq, dk, dv, total_q, total_k, strides))) return rc;
+  if (batch == 0 || (total_q == 0 && total_k == 0)) return ok();
+  const PlanLayout L = plan_layout(batch, total_q, total_k, true);
+  const size_t need = L.total + bwd_layout(total_q, hq, d).total;
+  if (ws == nullptr || ws_bytes < need || !aligned16(ws))
+    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* base = static_cast<char*>(ws);
+  const hipError_t e = build_plan(base, L, cu_q, cu_k, batch, total_q, total_k, hq, hkv, causal != 0, true, s);
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
+  return run_bwd(q, k, v, o, lse, dout, dq, dk, dv, batch, total_q, total_k, hq, hkv, d, strides, scale, causal,
+                 base, L, base + L.total, s);
+}
+
+int siq_attn_varlen_bwd_plan(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                             const void* dout, void* dq, void* dk, void* dv, int batch, int64_t total_q,
+                             int64_t total_k, int hq, int hkv, int d, const int64_t* strides, float scale, int causal,
+                             const void* plan, size_t plan_bytes, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_attn_common(batch, 0, 0, total_q, total_k, hq, hkv, d, scale);
+  if (rc) return rc;
+  if ((rc = check_bwd_tensors(q, k, v, o, lse, dout, dq, dk, dv, total_q, total_k, strides))) return rc;
+  if (batch == 0 || (total_q == 0 && total_k == 0)) return ok();
+  const PlanLayout L = plan_layout(batch, total_q, total_k, true);
+  if (plan == nullptr || plan_bytes < L.total || !aligned16(plan))
+    return fail(SIQ_ERR_WORKSPACE, "plan needs %zu bytes (16-byte aligned), got %zu", L.total, plan_bytes);
+  const size_t need = bwd_layout(total_q, hq, d).total;
+  if (ws == nullptr || ws_bytes < need || !aligned16(ws))
+    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
+  return run_bwd(q, k, v, o, lse, dout, dq, dk, dv, batch, total_q, total_k, hq, hkv, d, strides, scale, causal,
+                 static_cast<char*>(const_cast<void*>(plan)), L, static_cast<char*>(ws),
+                 static_cast<hipStream_t>(stream));
+}
+
+size_t siq_flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk_tokens, int need_dweight) {
+  if (n < 0 || hdim <= 0 || vocab <= 0) return 0;
+  return siq::flce_workspace_bytes(n, hdim, vocab, chunk_tokens, true, need_dweight != 0);
+}
+
+size_t siq_flce_loss_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab) {
+  if (n < 0 || hdim <= 0 || vocab <= 0) return 0;
+  return siq::flce_workspace_bytes(n, hdim, vocab, 1, false, false);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Shared by siq_flce_fwd_bwd (grads) and siq_flce_loss (loss only: no
+// dhidden / dweight).
+int flce_call(bool grads, const void* hidden, const void* weight, const int64_t* labels, int64_t n, int64_t hdim,
+              int64_t vocab, int64_t ignore_index, int reduction, const float* divisor, float* loss, int64_t* count,
+              int64_t* bad_labels, void* dhidden, void* dweight, int64_t chunk_tokens, void* ws, size_t ws_bytes,
+              void* stream) {
   if (n < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "n must be >= 0");
   if (hdim <= 0 || vocab <= 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "hdim and vocab must be positive");
   if (hdim % 64 != 0) return fail(SIQ_ERR_UNSUPPORTED, "hdim (%lld) must be a multiple of 64", (long long)hdim);
@@ -271,14 +388,16 @@ int siq_flce_fwd_bwd(const void* hidden, const void* weight, const int64_t* labe
   if (loss == nullptr || count == nullptr || bad_labels == nullptr)
     return fail(SIQ_ERR_INVALID_ARGUMENT, "loss, count and bad_labels must not be NULL");
   if (n > 0) {
-    if (hidden == nullptr || labels == nullptr || dhidden == nullptr)
-      return fail(SIQ_ERR_INVALID_ARGUMENT, "hidden, labels and dhidden must not be NULL");
-    if (!aligned16(hidden) || !aligned16(dhidden)) return fail(SIQ_ERR_ALIGNMENT, "hidden/dhidden not 16-byte aligned");
+    if (hidden == nullptr || labels == nullptr || (grads && dhidden == nullptr))
+      return fail(SIQ_ERR_INVALID_ARGUMENT, grads ? "hidden, labels and dhidden must not be NULL"
+                                                  : "hidden and labels must not be NULL");
+    if (!aligned16(hidden) || (grads && !aligned16(dhidden)))
+      return fail(SIQ_ERR_ALIGNMENT, "hidden/dhidden not 16-byte aligned");
   }
   if (weight == nullptr || !aligned16(weight)) return fail(SIQ_ERR_ALIGNMENT, "weight must be non-NULL and 16-byte aligned");
   if (dweight != nullptr && !aligned16(dweight)) return fail(SIQ_ERR_ALIGNMENT, "dweight not 16-byte aligned");
   if (chunk_tokens <= 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "chunk_tokens must be positive");
-  const size_t need = siq::flce_workspace_bytes(n, hdim, vocab, chunk_tokens, dweight != nullptr);
+  const size_t need = siq::flce_workspace_bytes(n, hdim, vocab, chunk_tokens, grads, dweight != nullptr);
   if (ws == nullptr || ws_bytes < need || !aligned16(ws))
     return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
   siq::FlceArgs a{};
@@ -294,6 +413,7 @@ int siq_flce_fwd_bwd(const void* hidden, const void* weight, const int64_t* labe
   a.loss = loss;
   a.count = count;
   a.bad_labels = bad_labels;
+  a.grads = grads;
   a.dhidden = static_cast<siq::bf16*>(dhidden);
   a.dweight = static_cast<siq::bf16*>(dweight);
   a.chunk = chunk_tokens;
@@ -301,6 +421,25 @@ int siq_flce_fwd_bwd(const void* hidden, const void* weight, const int64_t* labe
   const hipError_t e = siq::flce_run(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "fused CE launch failed: %s", hipGetErrorString(e));
   return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int siq_flce_fwd_bwd(const void* hidden, const void* weight, const int64_t* labels, int64_t n, int64_t hdim,
+                     int64_t vocab, int64_t ignore_index, int reduction, const float* divisor, float* loss,
+                     int64_t* count, int64_t* bad_labels, void* dhidden, void* dweight, int64_t chunk_tokens,
+                     void* ws, size_t ws_bytes, void* stream) {
+  return flce_call(true, hidden, weight, labels, n, hdim, vocab, ignore_index, reduction, divisor, loss, count,
+                   bad_labels, dhidden, dweight, chunk_tokens, ws, ws_bytes, stream);
+}
+
+int siq_flce_loss(const void* hidden, const void* weight, const int64_t* labels, int64_t n, int64_t hdim,
+                  int64_t vocab, int64_t ignore_index, int reduction, const float* divisor, float* loss,
+                  int64_t* count, int64_t* bad_labels, void* ws, size_t ws_bytes, void* stream) {
+  return flce_call(false, hidden, weight, labels, n, hdim, vocab, ignore_index, reduction, divisor, loss, count,
+                   bad_labels, nullptr, nullptr, 1, ws, ws_bytes, stream);
 }
 
 }  // extern "C"
@@ -513,13 +652,32 @@ int siq_gather_rows(const void* src, const int32_t* rows, int64_t n, int64_t hid
 }
 
 int siq_scale_bf16_inplace(void* data, int64_t numel, const float* scalar, void* stream) {
+  return siq_scale_bf16(data, data, numel, scalar, stream);
+}
+
+int siq_scale_bf16(const void* src, void* dst, int64_t numel, const float* scalar, void* stream) {
   if (numel < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "numel must be >= 0");
   if (numel == 0) return ok();
-  if (data == nullptr || scalar == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "data and scalar must not be NULL");
-  if (!aligned16(data)) return fail(SIQ_ERR_ALIGNMENT, "data not 16-byte aligned");
-  const hipError_t e = siq::launch_scale_bf16(static_cast<siq::bf16*>(data), numel, scalar,
-                                              static_cast<hipStream_t>(stream));
+  if (src == nullptr || dst == nullptr || scalar == nullptr)
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "src, dst and scalar must not be NULL");
+  if (!aligned16(src) || !aligned16(dst)) return fail(SIQ_ERR_ALIGNMENT, "src / dst not 16-byte aligned");
+  const hipError_t e = siq::launch_scale_bf16(static_cast<const siq::bf16*>(src), static_cast<siq::bf16*>(dst), numel,
+                                              scalar, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "scale launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int siq_probe_clock(uint64_t* out, int64_t spin_ticks, void* stream) {
+  if (out == nullptr || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(SIQ_ERR_ALIGNMENT, "out must be a non-NULL 8-byte aligned uint64[2]");
+  if (spin_ticks <= 0 || spin_ticks > 100000000)
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "spin_ticks must be in [1, 1e8] (ticks of 10 ns)");
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                              hipSuccess)
+    return fail(SIQ_ERR_LAUNCH, "cannot query the device");
+  const hipError_t e = siq::launch_clock_probe(out, spin_ticks, cus > 0 ? cus : 1, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "clock probe launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 

@@ -17,14 +17,15 @@ struct FlceArgs {
   float* loss;
   int64_t* count;
   int64_t* bad_labels;
+  bool grads;           // false: loss only (dhidden and dweight unused)
   bf16* dhidden;        // [n, hdim]
   bf16* dweight;        // [vocab, hdim] or nullptr
   int64_t chunk;        // tokens per logits chunk
   void* ws;
 };
 
-size_t flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk, bool need_dw);
+size_t flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk, bool need_dh, bool need_dw);
 hipError_t flce_run(const FlceArgs& a, hipStream_t stream);
-hipError_t launch_scale_bf16(bf16* data, int64_t numel, const float* scalar, hipStream_t stream);
+hipError_t launch_scale_bf16(const bf16* src, bf16* dst, int64_t numel, const float* scalar, hipStream_t stream);
 
 }  // namespace siq

@@ -28,8 +28,14 @@
 //     once for both gradient GEMMs.
 //  3. dH GEMM  dH_c^T = W^T dZ_c^T (split over the vocab) and
 //  4. dW GEMM  dW^T = H_c^T dZ_c.
-// With several chunks dW accumulates in an fp32 workspace.  Every reduction
-// has a fixed order, so results are bitwise reproducible.
+// With several chunks dW accumulates in an fp32 workspace; whether a chunk
+// starts, continues or finishes that sum is decided on the device from the
+// valid-row count, so chunks past the valid rows cost nothing.  Every
+// reduction has a fixed order, so results are bitwise reproducible.
+//
+// Loss only (no gradient wanted, e.g. evaluation under torch.no_grad): the
+// logits epilogue keeps its tile max / sum and z_y but stores no E, the row
+// pass stops at the loss, and neither gradient GEMM runs.
 #include "flce.h"
 #include "gemm.h"
 
@@ -52,6 +58,7 @@ struct LogitsArgs {
   const int64_t* nvalid;  // valid (compacted) rows in all chunks
   int64_t V, nc, nvt, c0;
   int nI, nJ;
+  int store_e;            // 0: loss only, E is not needed
 };
 
 __global__ __launch_bounds__(NT) void flce_logits_kernel(const LogitsArgs p) {
@@ -130,7 +137,7 @@ __global__ __launch_bounds__(NT) void flce_logits_kernel(const LogitsArgs p) {
           sum += e;
           e8[i] = (bf16)e;
         }
-        if (tv && v0 < p.V) st_bf16x8(p.E + tok * p.V + v0, e8);
+        if (p.store_e && tv && v0 < p.V) st_bf16x8(p.E + tok * p.V + v0, e8);
       }
     }
     sum = wave_sum_xor32(sum);
@@ -161,6 +168,7 @@ struct RowArgs {
   const float* invden;
   const int64_t* nvalid;
   int64_t nc, nvt, V, ignore_index, c0;
+  int rewrite;           // 0: loss only (E was never stored)
 };
 
 // One wave per token row.  lse2 = M + log2(sum_t s_t 2^(m_t - M)); then the
@@ -186,6 +194,7 @@ __global__ __launch_bounds__(256) void flce_row_kernel(const RowArgs p) {
   const bool valid = yv != p.ignore_index && yv >= 0 && yv < p.V;
   const float gv = valid ? *p.invden : 0.f;
   if (lane == 0) p.loss_row[row] = valid ? lse2 * kLn2 - p.zy[row] : 0.f;
+  if (!p.rewrite) return;
   // dZ, 8 columns per lane per chunk (V is a multiple of 8, so a chunk never
   // straddles the row end; 8 aligned columns never straddle a 256-column
   // tile).  An ignored row's dZ is zero: written without reading E.
@@ -333,9 +342,8 @@ struct DwArgs {
   bf16* dw;      // [V, hdim]
   float* acc32;  // [V, hdim] fp32 accumulator across chunks
   const int64_t* nvalid;
-  int64_t hdim, V, c0;
+  int64_t hdim, V, c0, chunk;
   int nI, nJ;
-  int mode;      // 0: bf16 store; 1: fp32 store; 2: fp32 add; 3: fp32 add + bf16 store
 };
 
 __global__ __launch_bounds__(NT) void flce_dw_kernel(const DwArgs p) {
@@ -343,9 +351,18 @@ __global__ __launch_bounds__(NT) void flce_dw_kernel(const DwArgs p) {
   int ti, tj;
   if (!tile_of(p.nI, p.nJ, p.nI, ti, tj)) return;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
+  // The chunk's part in the sum over chunks, from the valid-row count: the
+  // first chunk starts it, the one holding the last valid row finishes it
+  // (bf16 store), chunks past it do nothing.  A single chunk (or no valid
+  // row at all) stores bf16 directly.  mode 0: bf16 store; 1: fp32 store;
+  // 2: fp32 add; 3: fp32 add + bf16 store.
+  const int64_t nvt_all = *p.nvalid;
+  if (p.c0 > 0 && p.c0 >= nvt_all) return;
+  const bool last = p.c0 + p.chunk >= nvt_all;
+  const int mode = p.c0 == 0 ? (last ? 0 : 1) : (last ? 3 : 2);
   // tokens past the last 64-row step with a valid row are skipped (those up to
   // it are zero padding)
-  const int64_t nv = *p.nvalid - p.c0;
+  const int64_t nv = nvt_all - p.c0;
   const int64_t ke = min(p.Ht.rows, nv > 0 ? ((nv + BK - 1) / BK) * BK : (int64_t)0);
   f32x16 acc[4][2];
   gemm_core<false, false>(smem, p.Ht, p.Et, i0, j0, 0, ke, acc);
@@ -368,11 +385,11 @@ __global__ __launch_bounds__(NT) void flce_dw_kernel(const DwArgs p) {
           hi[i] = acc[a][b][8 * jj + 4 + i];
         }
         float* a32 = p.acc32 + v * p.hdim + hh;
-        if (p.mode >= 2) {
+        if (mode >= 2) {
           lo += *reinterpret_cast<const f32x4*>(a32);
           hi += *reinterpret_cast<const f32x4*>(a32 + 4);
         }
-        if (p.mode == 1 || p.mode == 2) {
+        if (mode == 1 || mode == 2) {
           *reinterpret_cast<f32x4*>(a32) = lo;
           *reinterpret_cast<f32x4*>(a32 + 4) = hi;
         } else {
@@ -492,6 +509,7 @@ __global__ __launch_bounds__(256) void flce_gather_kernel(const bf16* __restrict
     for (int64_t c = lane; c < nvec; c += 64)
       st_bf16x8(Hc + k * hdim + 8 * c, real ? ld_bf16x8(H + src * hdim + 8 * c) : zero_bf16x8());
   }
+  if (dh == nullptr) return;  // loss only
   for (int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < n; t += wstep) {
     const int64_t v = y[t];
     if (v != ignore_index && v >= 0 && v < V) continue;
@@ -515,18 +533,20 @@ __global__ __launch_bounds__(1024) void flce_loss_kernel(const float* __restrict
   if (threadIdx.x == 0) *loss = sm[0] * *invden;
 }
 
-__global__ __launch_bounds__(256) void scale_bf16_kernel(bf16* __restrict__ x, int64_t nvec, int64_t numel,
+// y = x * scalar in bf16 (rounded once from fp32).  x == y scales in place,
+// and then an exact 1.0 returns at once; out of place it is a copy.
+__global__ __launch_bounds__(256) void scale_bf16_kernel(const bf16* x, bf16* y, int64_t nvec, int64_t numel,
                                                          const float* __restrict__ scalar) {
   const float s = *scalar;
-  if (s == 1.f) return;
+  if (s == 1.f && x == y) return;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += (int64_t)gridDim.x * 256) {
     if (8 * i + 8 <= numel) {
       bf16x8 v = ld_bf16x8(x + 8 * i);
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[k] = (bf16)((float)v[k] * s);
-      st_bf16x8(x + 8 * i, v);
+      st_bf16x8(y + 8 * i, v);
     } else {
-      for (int64_t k = 8 * i; k < numel; ++k) x[k] = (bf16)((float)x[k] * s);
+      for (int64_t k = 8 * i; k < numel; ++k) y[k] = (bf16)((float)x[k] * s);
     }
   }
 }
@@ -552,8 +572,16 @@ int dh_splits(int64_t hdim, int64_t chunk) {
   return (int)s;
 }
 
-Layout layout(int64_t n, int64_t hdim, int64_t V, int64_t chunk, bool need_dw) {
+// need_dh false: loss only (no E, no gradient buffers); its chunks only bound
+// the per-(row, vocab tile) max / sum buffers, so they are large.
+constexpr int64_t kLossChunk = 32768;
+
+Layout layout(int64_t n, int64_t hdim, int64_t V, int64_t chunk, bool need_dh, bool need_dw) {
   Layout L{};
+  if (!need_dh) {
+    need_dw = false;
+    chunk = kLossChunk;
+  }
   L.chunk = chunk < n ? chunk : (n > 0 ? n : 1);
   L.nvt = (V + kVT - 1) / kVT;
   L.splits = dh_splits(hdim, L.chunk);
@@ -570,9 +598,9 @@ Layout layout(int64_t n, int64_t hdim, int64_t V, int64_t chunk, bool need_dw) {
   L.zy = off;
   off += al(sizeof(float) * (size_t)L.chunk);
   L.E = off;
-  off += al(sizeof(bf16) * (size_t)(L.chunk * V));
+  if (need_dh) off += al(sizeof(bf16) * (size_t)(L.chunk * V));
   L.part = off;
-  if (L.splits > 1) off += al(sizeof(float) * (size_t)(L.splits * L.chunk * hdim));
+  if (need_dh && L.splits > 1) off += al(sizeof(float) * (size_t)(L.splits * L.chunk * hdim));
   L.acc32 = off;
   if (need_dw && nchunks > 1) off += al(sizeof(float) * (size_t)(V * hdim));
   const int64_t npad = ((n > 0 ? n : 1) + 255) / 256 * 256;
@@ -588,13 +616,14 @@ Layout layout(int64_t n, int64_t hdim, int64_t V, int64_t chunk, bool need_dw) {
 
 }  // namespace
 
-size_t flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk, bool need_dw) {
+size_t flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk, bool need_dh, bool need_dw) {
   if (chunk <= 0) return 0;
-  return layout(n, hdim, vocab, chunk, need_dw).total;
+  return layout(n, hdim, vocab, chunk, need_dh, need_dw).total;
 }
 
 hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
-  const Layout L = layout(a.n, a.hdim, a.vocab, a.chunk, a.dweight != nullptr);
+  const bool grads = a.grads;
+  const Layout L = layout(a.n, a.hdim, a.vocab, a.chunk, grads, grads && a.dweight != nullptr);
   char* ws = static_cast<char*>(a.ws);
   float* invden = reinterpret_cast<float*>(ws + L.invden);
   float* loss_row = reinterpret_cast<float*>(ws + L.loss_row);
@@ -618,7 +647,7 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
     int64_t blocks = (a.n + 3) / 4;
     if (blocks > 4096) blocks = 4096;
     hipLaunchKernelGGL(flce_gather_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a.hidden, a.labels, rows,
-                       nvalid, a.n, Hd, V, a.ignore_index, hcomp, ycomp, a.dhidden);
+                       nvalid, a.n, Hd, V, a.ignore_index, hcomp, ycomp, grads ? a.dhidden : nullptr);
   }
   // chunks of compacted rows: the host sizes them for n rows; those past the
   // valid count return at once
@@ -644,6 +673,7 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
     lg.nvt = L.nvt;
     lg.nI = (int)L.nvt;
     lg.nJ = (int)((nc + BJ - 1) / BJ);
+    lg.store_e = grads ? 1 : 0;
     {
       const int total = lg.nI * lg.nJ;
       const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
@@ -664,7 +694,9 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
     rw.nvt = L.nvt;
     rw.V = V;
     rw.ignore_index = a.ignore_index;
+    rw.rewrite = grads ? 1 : 0;
     hipLaunchKernelGGL(flce_row_kernel, dim3((unsigned)((nc + 3) / 4)), dim3(256), 0, stream, rw);
+    if (!grads) continue;
 
     DhArgs dh{};
     dh.Wt = GOp{a.weight, Hd, V, Hd};
@@ -695,7 +727,7 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
                          nvalid, c0, nc, Hd, (int)L.splits);
     }
 
-    if (a.dweight != nullptr) {
+    if (grads && a.dweight != nullptr) {
       DwArgs dw{};
       dw.Ht = GOp{Hc, Hd, nc, Hd};
       dw.Et = GOp{E, V, nc, V};
@@ -707,16 +739,13 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
       dw.V = V;
       dw.nI = (int)((Hd + BI - 1) / BI);
       dw.nJ = (int)L.nvt;
-      if (nchunks == 1) dw.mode = 0;
-      else if (ci == 0) dw.mode = 1;
-      else if (ci + 1 < nchunks) dw.mode = 2;
-      else dw.mode = 3;
+      dw.chunk = L.chunk;
       const int total = dw.nI * dw.nJ;
       const int grid = ((total + kXcds - 1) / kXcds) * kXcds;
       hipLaunchKernelGGL(flce_dw_kernel, dim3(grid), dim3(NT), 0, stream, dw);
     }
   }
-  if (a.n == 0 && a.dweight != nullptr) {
+  if (grads && a.n == 0 && a.dweight != nullptr) {
     // no rows: d loss / d W is zero (a fill kernel, so the call stays graph-capturable)
     const int64_t nvec = V * Hd / 8;
     int64_t blocks = (nvec + 255) / 256;
@@ -727,11 +756,11 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_scale_bf16(bf16* data, int64_t numel, const float* scalar, hipStream_t stream) {
+hipError_t launch_scale_bf16(const bf16* src, bf16* dst, int64_t numel, const float* scalar, hipStream_t stream) {
   const int64_t nvec = (numel + 7) / 8;
   int64_t blocks = (nvec + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(scale_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, data, nvec, numel, scalar);
+  hipLaunchKernelGGL(scale_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, src, dst, nvec, numel, scalar);
   return hipGetLastError();
 }
 

@@ -11,10 +11,22 @@
 // Block 0 builds the q-tile list of the forward and dQ kernels (tiles of
 // `qrows` rows), heaviest first (work key: kv rows seen, in units of 64).  Block 1 builds the dK/dV
 // work items: a kv tile has n_rep x (q blocks that can see it) steps; tiles
-// with more than S = max(kMinSplitSteps, hkv total / kSplitTarget) steps are
-// cut into pieces of at most S steps, so that the longest item stays near the
-// average load of a CU; the pieces are placed heaviest first, and split tiles
-// are listed for the kernel that adds their partial sums.
+// with more than S steps are cut into pieces of at most S steps, so that the
+// longest item stays near the average load of a CU: S = hkv steps /
+// kSplitTarget (steps counted per kv-head), halved -- but not below
+// kLongPiece -- when that exceeds kLongPiece, and at least kMinSplitSteps.
+// The pieces are placed heaviest first, and split tiles are listed for the
+// kernel that adds their partial sums.
+//
+// Bounds (why the work lists and split slots always hold the schedule):
+//  * q tiles: sum_b ceil(L_b / qrows) <= total / qrows + batch < qcap;
+//  * S >= hkv * steps / (2 kSplitTarget), so a split tile (w > S steps) has
+//    np = ceil(w / S) < 2 w / S pieces: the extra items sum_split (np - 1) <
+//    steps / S <= 2 kSplitTarget / hkv, and the slots sum_split np * hkv <
+//    2 hkv steps / S <= 4 kSplitTarget;
+// both fit kv_item_cap and kSplitSlots.  The scheduler still checks every
+// placement and records an overflow in the plan header (status_q /
+// status_kv) instead of writing past a list.
 #include "attn.h"
 
 namespace siq {
@@ -110,7 +122,8 @@ __device__ int scan_global(int* a, int n, int* buf, int* wsum) {
 __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __restrict__ cu_q,
                                                                  const int* __restrict__ cu_k, int batch,
                                                                  int64_t total_q, int64_t total_k, int causal,
-                                                                 int n_rep, int hkv, SeqInfo* __restrict__ seq,
+                                                                 int n_rep, int hkv, PlanHeader* __restrict__ plan,
+                                                                 SeqInfo* __restrict__ seq,
                                                                  QTile* __restrict__ qtiles, int qrows, int qcap,
                                                                  KvItem* __restrict__ kvitems, int kvcap,
                                                                  int* __restrict__ seqbuf,
@@ -119,13 +132,14 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
   __shared__ int hist[kSchedKeys];
   __shared__ int wsum[kSchedThreads / 64 + 1];
   __shared__ long long wsteps[kSchedThreads / 64];
-  __shared__ int nslot, nsplit_sh;
+  __shared__ int nslot, nsplit_sh, status_sh;
   const int tid = threadIdx.x;
 
   for (int i = tid; i < kSchedKeys; i += kSchedThreads) hist[i] = 0;
   if (tid == 0) {
     nslot = 0;
     nsplit_sh = 0;
+    status_sh = 0;
   }
   __syncthreads();
 
@@ -145,9 +159,41 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
       for (int t = 0; t < nt; ++t) {
         const int pos = atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(s, t, qrows, causal)], 1);
         if (pos < qcap) qtiles[pos] = QTile{s, b, t, 0, 0};
+        else atomicOr(&status_sh, kStatusOverflow);
       }
     }
     for (int i = total + tid; i < qcap; i += kSchedThreads) qtiles[i] = QTile{SeqInfo{0, 0, 0, 0}, -1, -1, 0, 0};
+    __syncthreads();
+    if (tid == 0) {
+      PlanHeader h;
+      h.total_q = total_q;
+      h.total_k = total_k;
+      h.magic = kPlanMagic;
+      h.batch = batch;
+      h.n_rep = n_rep;
+      h.hkv = hkv;
+      h.causal = causal ? 1 : 0;
+      h.has_kv = kvitems != nullptr ? 1 : 0;
+      h.status_q = status_sh;
+      h.status_kv = 0;
+      h.status_use = 0;
+      h.pad = 0;
+      if (kvitems != nullptr) {
+        // block 1 owns status_kv: write every other field
+        plan->total_q = h.total_q;
+        plan->total_k = h.total_k;
+        plan->magic = h.magic;
+        plan->batch = h.batch;
+        plan->n_rep = h.n_rep;
+        plan->hkv = h.hkv;
+        plan->causal = h.causal;
+        plan->has_kv = h.has_kv;
+        plan->status_q = h.status_q;
+        plan->status_use = 0;
+      } else {
+        *plan = h;
+      }
+    }
     return;
   }
 
@@ -222,6 +268,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
       slot0 = atomicAdd(&nslot, np);
       const int k = atomicAdd(&nsplit_sh, 1);
       if (k < kMaxSplitTiles) splits[k] = SplitTile{b, t, np, slot0};
+      if (k >= kMaxSplitTiles || (slot0 + np) * hkv > kSplitSlots) atomicOr(&status_sh, kStatusOverflow);
     }
     for (int pc = 0; pc < np; ++pc) {
       const int pos = atomicAdd(&hist[kSchedKeys - 1 - clamp_key(min(S, w - pc * S))], 1);
@@ -236,6 +283,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
       it.slot0 = slot0;
       it.pad = 0;
       if (pos < kvcap) kvitems[pos] = it;
+      else atomicOr(&status_sh, kStatusOverflow);
     }
   }
   for (int i = total + tid; i < kvcap; i += kSchedThreads) {
@@ -244,18 +292,22 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
     kvitems[i] = it;
   }
   __syncthreads();
-  if (tid == 0) *nsplit = min(nsplit_sh, kMaxSplitTiles);
+  if (tid == 0) {
+    *nsplit = min(nsplit_sh, kMaxSplitTiles);
+    plan->status_kv = status_sh;
+  }
 }
 
 }  // namespace
 
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,
-                           int causal, int n_rep, int hkv, SeqInfo* seq, QTile* qtiles, int qrows, int qcap,
-                           KvItem* kvitems, int kvcap, int* seqbuf, SplitTile* splits, int* nsplit,
+                           int causal, int n_rep, int hkv, PlanHeader* plan, SeqInfo* seq, QTile* qtiles, int qrows,
+                           int qcap, KvItem* kvitems, int kvcap, int* seqbuf, SplitTile* splits, int* nsplit,
                            hipStream_t stream) {
   const int blocks = kvitems != nullptr ? 2 : 1;
   hipLaunchKernelGGL(schedule_kernel, dim3(blocks), dim3(kSchedThreads), 0, stream, cu_q, cu_k, batch, total_q,
-                     total_k, causal, n_rep, hkv, seq, qtiles, qrows, qcap, kvitems, kvcap, seqbuf, splits, nsplit);
+                     total_k, causal, n_rep, hkv, plan, seq, qtiles, qrows, qcap, kvitems, kvcap, seqbuf, splits,
+                     nsplit);
   return hipGetLastError();
 }
 

@@ -11,7 +11,9 @@ of ``Qwen2ForCausalLM.forward`` (transformers models/qwen2/modeling_qwen2.py:
   straight into ``fused_linear_cross_entropy`` with the labels shifted as
   ``ForCausalLMLoss`` shifts them (loss/loss_utils.py:63-64, or the given
   ``shift_labels``) and ``num_items_in_batch`` honoured; ``logits`` is None;
-* without ``labels`` (``generate``, evaluation): the original logits path.
+* without ``labels`` (``generate``): the original logits path;
+* with ``labels`` but no gradient (evaluation under ``torch.no_grad``): the
+  loss-only kernel, no logits and no gradient work.
 
 ``enable_fused_cross_entropy(model)`` installs it on a model instance (the
 ``SiQ_VLTextModel`` inside ``SiQ_VLForCausalLM``, or any Qwen2-style causal LM).
@@ -24,7 +26,7 @@ from typing import Any
 
 import torch
 
-from .cross_entropy import DEFAULT_CHUNK_TOKENS, IGNORE_INDEX, fused_linear_cross_entropy, shift_labels
+from .cross_entropy import IGNORE_INDEX, fused_linear_cross_entropy, shift_labels
 
 
 def fused_causal_lm_forward(self, input_ids=None, attention_mask=None, position_ids=None, past_key_values=None,
@@ -56,20 +58,21 @@ def fused_causal_lm_forward(self, input_ids=None, attention_mask=None, position_
         targets.reshape(-1).to(hidden.device),
         ignore_index=IGNORE_INDEX,
         num_items_in_batch=kwargs.get("num_items_in_batch"),
-        chunk_tokens=getattr(self, "siq_ce_chunk_tokens", DEFAULT_CHUNK_TOKENS),
+        chunk_tokens=getattr(self, "siq_ce_chunk_tokens", None),
     )
     return CausalLMOutputWithPast(loss=loss, logits=None, past_key_values=outputs.past_key_values,
                                   hidden_states=outputs.hidden_states, attentions=outputs.attentions)
 
 
-def enable_fused_cross_entropy(model: torch.nn.Module, chunk_tokens: int = DEFAULT_CHUNK_TOKENS) -> torch.nn.Module:
+def enable_fused_cross_entropy(model: torch.nn.Module, chunk_tokens: int | None = None) -> torch.nn.Module:
     """Routes ``model``'s loss through the fused kernel (in place); returns the
     module whose forward was replaced.  For ``SiQ_VLForCausalLM`` the text
-    model (``model.text_model``) is patched."""
+    model (``model.text_model``) is patched.  ``chunk_tokens`` None keeps the
+    default bound on the logits chunk."""
     target = getattr(model, "text_model", model)
     if not hasattr(target, "lm_head") or not hasattr(target, "model"):
         raise TypeError("expected a causal LM with .model (decoder) and .lm_head")
-    target.siq_ce_chunk_tokens = int(chunk_tokens)
+    target.siq_ce_chunk_tokens = None if chunk_tokens is None else int(chunk_tokens)
     target.forward = types.MethodType(fused_causal_lm_forward, target)
     return target
 

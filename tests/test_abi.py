@@ -59,6 +59,37 @@ def test_workspace_sizes(lib):
     assert a < 16384 * 151936 * 4
 
 
+def test_flce_default_workspace_bound_at_config4(lib):
+    """Config 4 at the default chunk: the softmax-numerator buffer stays within
+    its 2 GiB budget, below the bf16 logits of the batch (4.98 GB), and the
+    whole workspace (numerators, tile max / sum, split-K dH partials, the fp32
+    dW accumulator, compacted rows) within 4 GiB."""
+    from siq_vl_amd import cross_entropy as C
+
+    n, hdim, vocab = 16384, 1536, 151936
+    chunk = C.default_chunk_tokens(vocab)
+    assert chunk % 256 == 0 and 2 * chunk * vocab <= C.DEFAULT_E_BUDGET_BYTES
+    assert chunk == 6912
+    total = lib.siq_flce_workspace_bytes(n, hdim, vocab, chunk, 1)
+    one_chunk = lib.siq_flce_workspace_bytes(n, hdim, vocab, n, 1)
+    assert total <= 4 << 30, total
+    assert total < 2 * n * vocab  # the bf16 logits alone
+    assert one_chunk - total > (2 * (n - chunk) * vocab) // 2  # the bound is what shrank it
+    assert C.flce_workspace_bytes(n, hdim, vocab, None, True) == total
+    # loss only: no numerators at all
+    assert lib.siq_flce_loss_workspace_bytes(n, hdim, vocab) < 128 << 20
+
+
+def test_plan_sizes(lib):
+    assert lib.siq_attn_plan_bytes(-1, 10, 10) == 0
+    a, b = lib.siq_attn_plan_bytes(32, 16384, 16384), lib.siq_attn_plan_bytes(200, 32768, 32768)
+    assert 0 < a < b and a % 256 == 0
+    # the backward call's workspace is a plan plus the backward's own scratch
+    full = lib.siq_attn_bwd_workspace_bytes(32, 16384, 16384, 12, 2, 128)
+    own = lib.siq_attn_bwd_plan_workspace_bytes(32, 16384, 16384, 12, 2, 128)
+    assert full == a + own
+
+
 def _strides(n=16):
     return _lib.int64_array([128] * n)
 
@@ -110,6 +141,39 @@ def test_attention_bwd_validation(lib):
     assert rc == _lib.SIQ_ERR_INVALID_ARGUMENT and b"dq" in lib.siq_last_error()
 
 
+def test_plan_entry_validation(lib):
+    bp = lib.siq_attn_build_plan
+    assert bp(FAKE, FAKE, 2, 16, 16, 4, 2, 1, None, 0, None) == _lib.SIQ_ERR_WORKSPACE
+    assert bp(None, FAKE, 2, 16, 16, 4, 2, 1, FAKE, 1 << 20, None) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    assert bp(FAKE, FAKE, 2, 16, 16, 3, 2, 1, FAKE, 1 << 20, None) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    need = lib.siq_attn_plan_bytes(2, 16, 16)
+    fwd = lib.siq_attn_varlen_fwd_plan
+    assert fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, _strides(8), 0.1, 1, FAKE, need - 16,
+               None) == _lib.SIQ_ERR_WORKSPACE
+    assert fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 96, _strides(8), 0.1, 1, FAKE, need,
+               None) == _lib.SIQ_ERR_UNSUPPORTED
+    assert fwd(None, None, None, None, None, 0, 0, 0, 4, 2, 128, _strides(8), 0.1, 1, None, 0, None) == _lib.SIQ_OK
+    bwd = lib.siq_attn_varlen_bwd_plan
+    own = lib.siq_attn_bwd_plan_workspace_bytes(2, 16, 16, 4, 2, 128)
+    assert bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, _strides(16), 0.1, 1,
+               FAKE, need, FAKE, own - 16, None) == _lib.SIQ_ERR_WORKSPACE
+    assert bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, _strides(16), 0.1, 1,
+               None, need, FAKE, own, None) == _lib.SIQ_ERR_WORKSPACE
+
+
+def test_flce_loss_validation(lib):
+    f = lib.siq_flce_loss
+    need = lib.siq_flce_loss_workspace_bytes(16, 128, 1024)
+    assert f(FAKE, FAKE, FAKE, 16, 128, 1024, -100, 0, None, FAKE, FAKE, FAKE, FAKE, need - 256,
+             None) == _lib.SIQ_ERR_WORKSPACE
+    assert f(None, FAKE, FAKE, 16, 128, 1024, -100, 0, None, FAKE, FAKE, FAKE, FAKE, need,
+             None) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    assert f(FAKE, FAKE, FAKE, 16, 100, 1024, -100, 0, None, FAKE, FAKE, FAKE, FAKE, need,
+             None) == _lib.SIQ_ERR_UNSUPPORTED
+    assert f(FAKE, FAKE, FAKE, 16, 128, 1024, -100, 1, None, FAKE, FAKE, FAKE, FAKE, need,
+             None) == _lib.SIQ_ERR_INVALID_ARGUMENT
+
+
 def _flce(lib, **kw):
     args = dict(hidden=FAKE, weight=FAKE, labels=FAKE, n=16, hdim=128, vocab=1024, ignore_index=-100, reduction=0,
                 divisor=None, loss=FAKE, count=FAKE, bad=FAKE, dh=FAKE, dw=FAKE, chunk=8, ws=None, ws_bytes=0,
@@ -140,6 +204,9 @@ def test_scale_validation(lib):
     assert lib.siq_scale_bf16_inplace(None, 0, None, None) == _lib.SIQ_OK
     assert lib.siq_scale_bf16_inplace(None, -1, None, None) == _lib.SIQ_ERR_INVALID_ARGUMENT
     assert lib.siq_scale_bf16_inplace(FAKE + 2, 8, FAKE, None) == _lib.SIQ_ERR_ALIGNMENT
+    assert lib.siq_scale_bf16(FAKE, None, 8, FAKE, None) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    assert lib.siq_scale_bf16(FAKE, FAKE + 8, 8, FAKE, None) == _lib.SIQ_ERR_ALIGNMENT
+    assert lib.siq_scale_bf16(None, None, 0, None, None) == _lib.SIQ_OK
 
 
 def test_check_maps_status_to_exceptions():
