@@ -86,8 +86,17 @@ def validate_cu_seqlens(cu: torch.Tensor, total: int, name: str = "cu_seqlens") 
         raise ValueError(f"{name}[-1] ({vals[-1]}) must equal the number of packed tokens ({total})")
 
 
+def _norm_device(device) -> torch.device:
+    """``cuda`` -> ``cuda:<current index>`` (so that equal devices compare equal)."""
+    device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        return torch.device("cuda", torch.cuda.current_device())
+    return device
+
+
 def _device_cu(cu: torch.Tensor, device: torch.device, total: int, name: str) -> torch.Tensor:
     validate_cu_seqlens(cu, total, name)
+    device = _norm_device(device)
     if cu.device.type == "cpu":
         cu = cu.to(device, non_blocking=False)
     elif cu.device != device:
@@ -147,7 +156,7 @@ class AttnPlan:
 def build_attn_plan(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, total_q: int, total_k: int, hq: int,
                     hkv: int, causal: bool, device: torch.device | None = None) -> AttnPlan:
     """Builds a plan on the device (one small kernel, no host sync)."""
-    device = device or (cu_seqlens_q.device if cu_seqlens_q.device.type == "cuda" else torch.device("cuda"))
+    device = _norm_device(device or (cu_seqlens_q.device if cu_seqlens_q.device.type == "cuda" else "cuda"))
     cu_q = _device_cu(cu_seqlens_q, device, total_q, "cu_seqlens_q")
     cu_k = _device_cu(cu_seqlens_k, device, total_k, "cu_seqlens_k")
     if cu_q.numel() != cu_k.numel():
@@ -174,6 +183,7 @@ def cached_attn_plan(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, tot
     ``cu_seqlens_q`` tensor object itself (so it lives exactly as long as
     that tensor); an in-place change of either offsets tensor (its
     ``_version``) or other totals / heads / causality build a new one."""
+    device = _norm_device(device)
     key = (cu_seqlens_q._version, cu_seqlens_k._version, int(total_q), int(total_k), int(hq) // int(hkv), int(hkv),
            bool(causal), str(device))
     cache = getattr(cu_seqlens_q, _PLAN_ATTR, None)
@@ -196,7 +206,7 @@ def cached_attn_plan(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, tot
 def _resolve_plan(plan, cu_seqlens_q, cu_seqlens_k, total_q, total_k, hq, hkv, causal, device) -> AttnPlan:
     if plan is None:
         return cached_attn_plan(cu_seqlens_q, cu_seqlens_k, total_q, total_k, hq, hkv, causal, device)
-    if not plan.matches(plan.batch, total_q, total_k, hq, hkv, causal) or plan.buf.device != device:
+    if not plan.matches(plan.batch, total_q, total_k, hq, hkv, causal) or plan.buf.device != _norm_device(device):
         raise ValueError("the attention plan was built for other sequences, heads or causality")
     return plan
 
