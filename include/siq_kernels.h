@@ -99,6 +99,23 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
                         int64_t total_q, int64_t total_k, int hq, int hkv, int d, const int64_t* strides,
                         float softmax_scale, int causal, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free siq_attn_varlen_fwd.  No counterpart in the reference: it
+ * exists for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation) and takes
+ * no workspace.  Same arguments (minus the workspace), validation and output,
+ * bitwise, as siq_attn_varlen_fwd.  The batch's plan goes to a static device
+ * array of 1 MiB per GPU (held until the process ends): batch and total_q
+ * must satisfy 256 + 16 batch + 32 (total_q / 128 + batch + 1) <= 1 MiB (each
+ * term rounded up to 256 bytes), e.g. batch <= 8192 with total_q <= 2^20;
+ * larger calls return SIQ_ERR_WORKSPACE before anything is launched.  All
+ * calls on one GPU share the array: calls that overlap on one GPU (from
+ * different streams or threads) race. */
+int siq_attn_varlen_fwd_noalloc(const void* q, const void* k, const void* v, void* o, float* lse,
+                                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int batch,
+                                int max_seqlen_q, int max_seqlen_k, int64_t total_q, int64_t total_k, int hq,
+                                int hkv, int d, const int64_t* strides, float softmax_scale, int causal,
+                                void* stream);
+
 /* ---------------------------------------------------------------------------
  * Attention plans: the schedule of one packed batch, built once and reused.
  *

@@ -45,6 +45,11 @@ _PROTOS = {
          _c_void_p, _c_void_p, _i32, _i32, _i32, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_i64), _f32, _i32,
          _c_void_p, _size, _c_void_p],
     ),
+    "siq_attn_varlen_fwd_noalloc": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i64, _i64,
+         _i32, _i32, _i32, ctypes.POINTER(_i64), _f32, _i32, _c_void_p],
+    ),
     "siq_attn_plan_bytes": (_size, [_i32, _i64, _i64]),
     "siq_attn_bwd_plan_workspace_bytes": (_size, [_i32, _i64, _i64, _i32, _i32, _i32]),
     "siq_attn_build_plan": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _i64, _i32, _i32, _i32, _c_void_p, _size,

@@ -10,15 +10,18 @@
 
 #include "../../include/siq_kernels.h"
 #include "attn.h"
+#include "capi_internal.h"
 #include "flce.h"
 #include "probe.h"
 #include "proj.h"
 #include "rope.h"
 #include "splice.h"
 
-namespace {
+namespace siq_capi {
 
+namespace {
 thread_local std::string g_last_error;
+}  // namespace
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -38,14 +41,6 @@ int ok() {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
-
-// An attention plan: header, per-sequence extents, the q-tile list (forward,
-// dQ) and the dK/dV work items with their split tiles.  It depends on the
-// sequences, the head counts and causality, not on the tensors.
-struct PlanLayout {
-  size_t header, seq, qtiles, kvitems, seqbuf, splits, nsplit, total;
-  int qcap, kvcap;
-};
 
 PlanLayout plan_layout(int batch, int64_t total_q, int64_t total_k, bool kv) {
   PlanLayout L{};
@@ -133,7 +128,9 @@ int check_tensor(const char* name, const void* p, const int64_t* st, bool need) 
   return SIQ_OK;
 }
 
-}  // namespace
+}  // namespace siq_capi
+
+using namespace siq_capi;
 
 extern "C" {
 
@@ -181,7 +178,7 @@ int siq_attn_build_plan(const int32_t* cu_q, const int32_t* cu_k, int batch, int
 
 }  // extern "C"
 
-namespace {
+namespace siq_capi {
 
 // Fills the plan pointers of p from a plan laid out by L at base.
 void set_plan(siq::AttnParams& p, char* base, const PlanLayout& L) {
@@ -281,7 +278,9 @@ int run_bwd(const void* q, const void* k, const void* v, const void* o, const fl
   return ok();
 }
 
-}  // namespace
+}  // namespace siq_capi
+
+using namespace siq_capi;
 
 extern "C" {
 
