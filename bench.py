@@ -252,6 +252,81 @@ def bench_rope(steps: int, warmup: int) -> dict:
             "fwd_gbs": nbytes / (fwd_ms * 1e-3) / 1e9, "bwd_gbs": nbytes / (bwd_ms * 1e-3) / 1e9}
 
 
+def graphed_ms(fn, reps: int, steps: int, warmup: int) -> float:
+    """Median ms of one ``fn()`` call: ``reps`` calls captured in a HIP graph,
+    replayed ``steps`` times after ``warmup`` replays (events on the launch
+    stream).  For steps made of short kernels whose host launch cost would
+    otherwise be timed."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    for _ in range(max(warmup, 1)):
+        g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = _events(steps + 1)
+    ev[0].record(stream)
+    for i in range(steps):
+        g.replay()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    return _median([ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]) / reps
+
+
+def bench_rope_attention(steps: int, warmup: int) -> dict:
+    """Config 2 with the decoder's RoPE in the step (plan built once per batch,
+    outside): the unfused pipeline (RoPE of q and k, attention fwd + bwd, RoPE
+    backward), the drop-in (the rotation's backward of dq inside the dQ
+    kernel, k-only RoPE backward) and the fully fused variant (q also rotated
+    inside the attention forward); all bitwise the same results.  Each step
+    is graph-replayed: several of its kernels are shorter than their launch."""
+    cfg = W.attn_config(2)
+    dev = torch.device("cuda")
+    x = W.attn_inputs(cfg, device=dev)
+    cu = cfg.cu_seqlens().to(dev)
+    t, d = cfg.total, cfg.d
+    pos = torch.cat([torch.arange(n) for n in cfg.lengths]).float()
+    inv = 1.0 / (1000000.0 ** (torch.arange(0, d, 2).float() / d))
+    emb = torch.cat([pos[:, None] * inv, pos[:, None] * inv], dim=-1)
+    cos, sin = emb.cos().to(torch.bfloat16).to(dev), emb.sin().to(torch.bfloat16).to(dev)
+    scale = d**-0.5
+    plan = A.build_attn_plan(cu, cu, t, t, cfg.hq, cfg.hkv, True, dev)
+    q, k, v, do = x["q"], x["k"], x["v"], x["dout"]
+
+    def unfused():
+        qe, ke = R.rope_fwd(q[None], k[None], cos[None], sin[None])
+        out, lse = A.varlen_attn_fwd(qe[0], ke[0], v, cu, cu, 0, 0, scale, True, plan=plan)
+        dqe, dke, _ = A.varlen_attn_bwd(do, qe[0], ke[0], v, out, lse, cu, cu, 0, 0, scale, True, plan=plan)
+        R.rope_bwd(dqe[None], dke[None], cos[None], sin[None])
+
+    def dropin():
+        qe, ke = R.rope_fwd(q[None], k[None], cos[None], sin[None])
+        out, lse = A.varlen_attn_fwd(qe[0], ke[0], v, cu, cu, 0, 0, scale, True, plan=plan)
+        _, dke, _ = A.varlen_attn_rope_bwd(do, qe[0], ke[0], v, out, lse, cos, sin, cu, cu, 0, 0, scale, True,
+                                           plan=plan)
+        R.rotate_k_backward(dke, cos, sin)
+
+    def fused_fwd():
+        ke = R.rotate_k(k[None], cos[None], sin[None])[0]
+        out, lse, qe = A.varlen_attn_rope_fwd(q, ke, v, cos, sin, cu, cu, 0, 0, scale, True, plan=plan)
+        _, dke, _ = A.varlen_attn_rope_bwd(do, qe, ke, v, out, lse, cos, sin, cu, cu, 0, 0, scale, True,
+                                           plan=plan)
+        R.rotate_k_backward(dke, cos, sin)
+
+    def attention_only():
+        out, lse = A.varlen_attn_fwd(q, k, v, cu, cu, 0, 0, scale, True, plan=plan)
+        A.varlen_attn_bwd(do, q, k, v, out, lse, cu, cu, 0, 0, scale, True, plan=plan)
+
+    res = {}
+    for name, fn in (("attention_only", attention_only), ("unfused", unfused), ("dropin", dropin),
+                     ("fused_fwd", fused_fwd)):
+        res[name + "_ms"] = graphed_ms(fn, 5, steps, warmup)
+    return res
+
+
 def bench_projector(steps: int, warmup: int) -> dict:
     """Pixel-shuffle projector forward + backward (dx and dweight) at the production
     shape: 16 SigLIP2-large-512 tiles (32 x 32 patches x 1024) -> Qwen2.5-1.5B (1536),
@@ -533,6 +608,13 @@ def main() -> int:
               f"{rope['bwd_ms'] * 1e3:.1f} us ({rope['bwd_gbs']:.0f} GB/s) in a graph; one eager call "
               f"{rope['eager_fwd_ms'] * 1e3:.1f} us; reference torch ops fwd+bwd {rope['ref_ms'] * 1e3:.1f} us",
               file=sys.stderr, flush=True)
+    ropeattn = None
+    if not args.skip_rope:
+        ropeattn = bench_rope_attention(leg_steps, args.warmup)
+        print(f"[bench] config 2 with RoPE (graph-replayed): attention alone {ropeattn['attention_only_ms'] * 1e3:.1f} "
+              f"us, unfused {ropeattn['unfused_ms'] * 1e3:.1f} us, drop-in (dq rotation in the dQ kernel) "
+              f"{ropeattn['dropin_ms'] * 1e3:.1f} us, q also rotated in the forward {ropeattn['fused_fwd_ms'] * 1e3:.1f} "
+              f"us", file=sys.stderr, flush=True)
     proj = None
     if not args.skip_projector:
         proj = bench_projector(leg_steps, args.warmup)
@@ -614,6 +696,17 @@ def main() -> int:
                                      "algorithmic_bytes": rope["bytes"]},
                         "bwd_gbs": round(rope["bwd_gbs"], 1),
                         "reference_torch_ops_fwd_bwd_us": round(rope["ref_ms"] * 1e3, 2)}
+    if ropeattn is not None:
+        line["rope_attention"] = {
+            "workload": "config 2 step with the decoder's RoPE, plan built outside, graph-replayed: unfused = "
+                        "RoPE(q, k) + attention fwd + bwd + RoPE bwd; dropin = the same with the rotation's backward "
+                        "of dq inside the dQ kernel and a k-only RoPE bwd; fused_fwd = q also rotated inside the "
+                        "attention forward (k-only RoPE fwd); all bitwise the same outputs",
+            "attention_only_us": round(ropeattn["attention_only_ms"] * 1e3, 2),
+            "unfused_us": round(ropeattn["unfused_ms"] * 1e3, 2), "dropin_us": round(ropeattn["dropin_ms"] * 1e3, 2),
+            "fused_fwd_us": round(ropeattn["fused_fwd_ms"] * 1e3, 2),
+            "rope_round_trip_unfused_us": round((ropeattn["unfused_ms"] - ropeattn["attention_only_ms"]) * 1e3, 2),
+            "rope_cost_dropin_us": round((ropeattn["dropin_ms"] - ropeattn["attention_only_ms"]) * 1e3, 2)}
     if proj is not None:
         line["projector"] = {
             "workload": "pixel-shuffle projector fwd+bwd (dx, dweight): 16 tiles x 32x32 patches x 1024 -> r 2 -> "

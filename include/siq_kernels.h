@@ -152,6 +152,32 @@ int siq_attn_varlen_bwd_plan(const void* q, const void* k, const void* v, const 
                              int causal, const void* plan, size_t plan_bytes, void* workspace,
                              size_t workspace_bytes, void* stream);
 
+/* Varlen attention with the decoder's rotary embedding of q fused in.
+ *
+ * Replaces apply_rotary_pos_emb's q half (transformers modeling_qwen2.py:
+ * 105-135, called at :206-211) together with the attention call after it:
+ * siq_attn_rope_fwd_plan reads q BEFORE rotation, rotates it in registers with
+ * the cos / sin rows of each token (bitwise siq_rope_fwd's q_embed), attends
+ * as siq_attn_varlen_fwd_plan does (k already rotated, e.g. by siq_rope_fwd
+ * with hq = 0) and writes the rotated q to q_embed for the backward.
+ * siq_attn_rope_bwd_plan takes that q_embed and writes dq with respect to the
+ * q BEFORE rotation (bitwise siq_rope_bwd applied to siq_attn_varlen_bwd_plan's
+ * dq); dk, dv are those of siq_attn_varlen_bwd_plan (dk with respect to the
+ * rotated k).  cos / sin: [total_q, d] bf16 rows, one per packed token.
+ * strides: fwd[12] = the 8 of siq_attn_varlen_fwd, q_embed (tok, head),
+ * cos_tok, sin_tok; bwd[18] = the 16 of siq_attn_varlen_bwd (q = q_embed),
+ * cos_tok, sin_tok. */
+int siq_attn_rope_fwd_plan(const void* q, const void* k, const void* v, void* o, float* lse, void* q_embed,
+                           const void* cos, const void* sin, int batch, int64_t total_q, int64_t total_k, int hq,
+                           int hkv, int d, const int64_t* strides, float softmax_scale, int causal, const void* plan,
+                           size_t plan_bytes, void* stream);
+
+int siq_attn_rope_bwd_plan(const void* q_embed, const void* k, const void* v, const void* o, const float* lse,
+                           const void* dout, void* dq, void* dk, void* dv, const void* cos, const void* sin, int batch,
+                           int64_t total_q, int64_t total_k, int hq, int hkv, int d, const int64_t* strides,
+                           float softmax_scale, int causal, const void* plan, size_t plan_bytes, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Fused linear cross-entropy (lm_head + loss), forward and backward.
  *
@@ -226,7 +252,9 @@ int siq_scale_bf16_inplace(void* data, int64_t numel, const float* scalar, void*
  * dk_embed, cos, sin, dq, dk.  Strides are multiples of 8 elements and base
  * pointers 16-byte aligned.  An output may be its input (same pointer and
  * strides, in place); any other overlap is undefined.  head_dim: a multiple of
- * 16 in [16, 512]; hq, hkv <= 4096; batch * seqlen < 2^32.
+ * 16 in [16, 512]; hq, hkv <= 4096; batch * seqlen < 2^32.  hq = 0 rotates k
+ * only (q and its output are then not read and may be NULL): the pass that
+ * goes with siq_attn_rope_fwd_plan / _bwd_plan, which rotate q themselves.
  * No workspace.
  * ------------------------------------------------------------------------- */
 int siq_rope_fwd(const void* q, const void* k, const void* cos, const void* sin, void* q_embed, void* k_embed,

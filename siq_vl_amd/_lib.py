@@ -65,6 +65,17 @@ _PROTOS = {
          _i32, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_i64), _f32, _i32, _c_void_p, _size, _c_void_p, _size,
          _c_void_p],
     ),
+    "siq_attn_rope_fwd_plan": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i64,
+         _i32, _i32, _i32, ctypes.POINTER(_i64), _f32, _i32, _c_void_p, _size, _c_void_p],
+    ),
+    "siq_attn_rope_bwd_plan": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _i32, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_i64), _f32, _i32, _c_void_p,
+         _size, _c_void_p, _size, _c_void_p],
+    ),
     "siq_flce_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i32]),
     "siq_flce_fwd_bwd": (
         _i32,

@@ -286,6 +286,142 @@ class _VarlenAttnFn(torch.autograd.Function):
         return dq, dk, dv, None, None, None, None, None, None
 
 
+def _check_rope_rows(cos: torch.Tensor, sin: torch.Tensor, total_q: int, d: int) -> None:
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dim() != 2 or t.shape[0] != total_q or t.shape[1] != d:
+            raise ValueError(f"{name} must be [total_q, head_dim] = [{total_q}, {d}], got {tuple(t.shape)}")
+        if t.dtype != torch.bfloat16 or t.device.type != "cuda":
+            raise ValueError(f"{name} must be a bf16 GPU tensor")
+        if t.stride(1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
+            raise ValueError(f"{name} rows must be contiguous and 16-byte aligned")
+
+
+def varlen_attn_rope_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                         cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
+                         max_seqlen_k: int, softmax_scale: float, causal: bool,
+                         plan: AttnPlan | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Attention with the decoder's rotary embedding of q fused in
+    (``siq_attn_rope_fwd_plan``): ``q`` is the query BEFORE rotation, ``k`` the
+    key after it, ``cos`` / ``sin`` ``[total_q, d]`` rows per token.  Returns
+    ``(out, lse, q_embed)``; ``q_embed`` (the rotated q, bitwise
+    ``rope_fwd``'s) is what the backward reads."""
+    hq, hkv, d = _check_common(q, k, v)
+    total_q, total_k = q.shape[0], k.shape[0]
+    _check_rope_rows(cos, sin, total_q, d)
+    pl = _resolve_plan(plan, cu_seqlens_q, cu_seqlens_k, total_q, total_k, hq, hkv, causal, q.device)
+    out = torch.empty((total_q, hq, d), dtype=q.dtype, device=q.device)
+    lse = torch.empty((hq, total_q), dtype=torch.float32, device=q.device)
+    qe = torch.empty((total_q, hq, d), dtype=q.dtype, device=q.device)
+    strides = _lib.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+                                out.stride(0), out.stride(1), qe.stride(0), qe.stride(1), cos.stride(0),
+                                sin.stride(0)])
+    rc = _lib.lib().siq_attn_rope_fwd_plan(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                           qe.data_ptr(), cos.data_ptr(), sin.data_ptr(), pl.batch, total_q, total_k,
+                                           hq, hkv, d, strides, float(softmax_scale), int(bool(causal)),
+                                           pl.buf.data_ptr(), pl.buf.numel(), _stream(q.device))
+    _lib.check(rc, "siq_attn_rope_fwd_plan")
+    return out, lse, qe
+
+
+def varlen_attn_rope_bwd(dout: torch.Tensor, q_embed: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                         out: torch.Tensor, lse: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                         cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
+                         max_seqlen_k: int, softmax_scale: float, causal: bool,
+                         plan: AttnPlan | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Backward of ``varlen_attn_rope_fwd`` (``siq_attn_rope_bwd_plan``):
+    ``(dq, dk, dv)`` with dq for the q BEFORE rotation (bitwise ``rope_bwd``
+    of the unfused dq), dk for the rotated k."""
+    hq, hkv, d = _check_common(q_embed, k, v)
+    total_q, total_k = q_embed.shape[0], k.shape[0]
+    _check_token_major("out", out, heads=hq, dim=d)
+    _check_token_major("dout", dout, heads=hq, dim=d)
+    if out.shape[0] != total_q or dout.shape[0] != total_q:
+        raise ValueError("out / dout must have total_q rows")
+    if lse.shape != (hq, total_q) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError(f"lse must be a contiguous fp32 [{hq}, {total_q}] tensor")
+    _check_rope_rows(cos, sin, total_q, d)
+    pl = _resolve_plan(plan, cu_seqlens_q, cu_seqlens_k, total_q, total_k, hq, hkv, causal, q_embed.device)
+    dq = torch.empty((total_q, hq, d), dtype=q_embed.dtype, device=q_embed.device)
+    dk = torch.empty((total_k, hkv, d), dtype=q_embed.dtype, device=q_embed.device)
+    dv = torch.empty((total_k, hkv, d), dtype=q_embed.dtype, device=q_embed.device)
+    L = _lib.lib()
+    ws_bytes = L.siq_attn_bwd_plan_workspace_bytes(pl.batch, total_q, total_k, hq, hkv, d)
+    ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=q_embed.device)
+    q = q_embed
+    strides = _lib.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+                                out.stride(0), out.stride(1), dout.stride(0), dout.stride(1), dq.stride(0),
+                                dq.stride(1), dk.stride(0), dk.stride(1), dv.stride(0), dv.stride(1), cos.stride(0),
+                                sin.stride(0)])
+    rc = L.siq_attn_rope_bwd_plan(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                  dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), cos.data_ptr(),
+                                  sin.data_ptr(), pl.batch, total_q, total_k, hq, hkv, d, strides,
+                                  float(softmax_scale), int(bool(causal)), pl.buf.data_ptr(), pl.buf.numel(),
+                                  ws.data_ptr(), ws.numel(), _stream(q.device))
+    _lib.check(rc, "siq_attn_rope_bwd_plan")
+    return dq, dk, dv
+
+
+class _VarlenRopeAttnFn(torch.autograd.Function):
+    """apply_rotary_pos_emb(q, k) followed by attention, as one autograd node.
+
+    Forward: one RoPE pass over q and k (its q_embed is what the backward's
+    dK/dV kernel stages from memory anyway), then the attention forward.
+    Backward: the rotation's backward of dq is fused into the dQ kernel's
+    store epilogue (dq of the q before rotation leaves the kernel directly;
+    dq_embed never reaches memory) and k's goes through a k-only RoPE pass.
+    Measured on MI355X at the config-2 shape this split beats both the
+    unfused pair and rotating q inside the attention forward as well
+    (``varlen_attn_rope_fwd``), whose extra q_embed stores and rotation sit
+    on every workgroup's critical path."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cos, sin, cu_q, cu_k, max_q, max_k, scale, causal):
+        from . import rope as _rope
+
+        cos, sin = cos.contiguous(), sin.contiguous()
+        qe, ke = _rope.rope_fwd(q[None], k[None], cos[None], sin[None])
+        qe, ke = qe[0], ke[0]
+        v = _ensure_token_major(v)
+        hq, hkv = qe.shape[1], ke.shape[1]
+        plan = cached_attn_plan(cu_q, cu_k, qe.shape[0], ke.shape[0], hq, hkv, causal, qe.device)
+        out, lse = varlen_attn_fwd(qe, ke, v, cu_q, cu_k, max_q, max_k, scale, causal, plan=plan)
+        ctx.save_for_backward(qe, ke, v, out, lse, cos, sin)
+        ctx.plan = plan
+        ctx.args = (max_q, max_k, scale, causal)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        from . import rope as _rope
+
+        qe, ke, v, out, lse, cos, sin = ctx.saved_tensors
+        max_q, max_k, scale, causal = ctx.args
+        plan = ctx.plan
+        dq, dke, dv = varlen_attn_rope_bwd(_ensure_token_major(dout), qe, ke, v, out, lse, cos, sin, plan.cu_q,
+                                           plan.cu_k, max_q, max_k, scale, causal, plan=plan)
+        dk = _rope.rotate_k_backward(dke, cos, sin)
+        return dq, dk, dv, None, None, None, None, None, None, None, None
+
+
+def flash_attn_varlen_rope_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                                sin: torch.Tensor, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
+                                max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float | None = None,
+                                causal: bool = False) -> torch.Tensor:
+    """``flash_attn_varlen_func(*apply_rotary_pos_emb(q, k, cos, sin), v)`` as
+    one op: ``q [total, hq, d]`` and ``k [total, hkv, d]`` BEFORE rotation
+    (self-attention: q and k rows are the same tokens), ``cos`` / ``sin
+    [total, d]`` the rows of each packed token.  Output and gradients are
+    bitwise those of the two separate ops."""
+    if cos.requires_grad or sin.requires_grad:
+        raise ValueError("gradients with respect to cos / sin are not supported")
+    if q.shape[0] != k.shape[0]:
+        raise ValueError("the fused rotary attention needs q and k rows of the same tokens")
+    if softmax_scale is None:
+        softmax_scale = q.shape[-1] ** -0.5
+    return _VarlenRopeAttnFn.apply(q, k, v, cos, sin, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
+                                   int(max_seqlen_k), float(softmax_scale), bool(causal))
+
+
 def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
                            cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int, dropout_p: float = 0.0,
                            softmax_scale: float | None = None, causal: bool = False,
@@ -368,6 +504,64 @@ def _unpad_from_mask(mask2d: torch.Tensor, s_k: int) -> tuple[torch.Tensor, torc
     return _cached_derived(mask2d, f"mask{s_k}", make)
 
 
+def _attend_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, attention_mask: torch.Tensor | None,
+                   is_causal: bool, scaling: float, kwargs: dict, rope=None) -> torch.Tensor:
+    """q ``[B, S_q, Hq, D]``, k / v ``[B, S_k, Hkv, D]`` (bf16 token-major views)
+    -> out ``[B, S_q, Hq, D]``.  Packing is read, in order, from
+    ``cu_seq_lens_q/k`` + ``max_length_q/k`` kwargs, from a 2-D padding
+    ``attention_mask`` (rows are unpadded), from restarting ``position_ids``
+    (B == 1); otherwise every batch row is one sequence.  ``rope`` = (cos, sin)
+    ``[B or 1, S_q, D]``: q and k arrive before rotation and are rotated by
+    the attention op (``flash_attn_varlen_rope_func``)."""
+    bsz, s_q, hq, d = q.shape
+    s_k, hkv = k.shape[1], k.shape[2]
+    cos_t = sin_t = None
+    if rope is not None:
+        cos, sin = rope
+        cos_t = cos.expand(bsz, s_q, d).reshape(bsz * s_q, d).contiguous()
+        sin_t = sin.expand(bsz, s_q, d).reshape(bsz * s_q, d).contiguous()
+
+    def attend(qf, kf, vf, cu_q, cu_k, mq, mk, cs=None, sn=None):
+        if cs is None:
+            return flash_attn_varlen_func(qf, kf, vf, cu_q, cu_k, mq, mk, softmax_scale=scaling, causal=is_causal)
+        return flash_attn_varlen_rope_func(qf, kf, vf, cs, sn, cu_q, cu_k, mq, mk, softmax_scale=scaling,
+                                           causal=is_causal)
+
+    cu_q = kwargs.get("cu_seq_lens_q")
+    cu_k = kwargs.get("cu_seq_lens_k")
+    max_q = kwargs.get("max_length_q")
+    max_k = kwargs.get("max_length_k")
+    position_ids = kwargs.get("position_ids")
+    if cu_q is not None and cu_k is not None and max_q is not None and max_k is not None:
+        out = attend(q.reshape(-1, hq, d), k.reshape(-1, hkv, d), v.reshape(-1, hkv, d), cu_q.to(torch.int32),
+                     cu_k.to(torch.int32), int(max_q), int(max_k), cos_t, sin_t)
+        return out.reshape(bsz, s_q, hq, d)
+    if attention_mask is not None and attention_mask.dim() == 2:
+        cu, idx, maxlen = _unpad_from_mask(attention_mask, s_k)
+        if s_q != s_k:
+            raise ValueError("padded (unpacked) inputs need equal query and key lengths")
+        qu = q.reshape(-1, hq, d).index_select(0, idx)
+        ku = k.reshape(-1, hkv, d).index_select(0, idx)
+        vu = v.reshape(-1, hkv, d).index_select(0, idx)
+        cu_cs = None if cos_t is None else cos_t.index_select(0, idx)
+        cu_sn = None if sin_t is None else sin_t.index_select(0, idx)
+        ou = attend(qu, ku, vu, cu, cu, maxlen, maxlen, cu_cs, cu_sn)
+        out = torch.zeros((bsz * s_q, hq, d), dtype=ou.dtype, device=ou.device)
+        return out.index_copy(0, idx, ou).reshape(bsz, s_q, hq, d)
+    if position_ids is not None and bsz == 1 and s_q == s_k:
+        cu, maxlen = _cu_from_position_ids(position_ids)
+        out = attend(q.reshape(-1, hq, d), k.reshape(-1, hkv, d), v.reshape(-1, hkv, d), cu, cu, maxlen, maxlen,
+                     cos_t, sin_t)
+        return out.reshape(bsz, s_q, hq, d)
+    if attention_mask is not None:
+        raise ValueError("siq_varlen expects a 2-D padding mask or None (register its mask interface)")
+    cu_q = torch.arange(0, (bsz + 1) * s_q, s_q, dtype=torch.int32, device=q.device)
+    cu_k = cu_q if s_k == s_q else torch.arange(0, (bsz + 1) * s_k, s_k, dtype=torch.int32, device=q.device)
+    out = attend(q.reshape(-1, hq, d), k.reshape(-1, hkv, d), v.reshape(-1, hkv, d), cu_q, cu_k, s_q, s_k, cos_t,
+                 sin_t)
+    return out.reshape(bsz, s_q, hq, d)
+
+
 def siq_varlen_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: torch.Tensor,
                                  value: torch.Tensor, attention_mask: torch.Tensor | None, dropout: float = 0.0,
                                  scaling: float | None = None, sliding_window: int | None = None,
@@ -377,8 +571,8 @@ def siq_varlen_attention_forward(module: torch.nn.Module, query: torch.Tensor, k
     -> ``(out [B, S, Hq, D] contiguous, None)``.
 
     Packing is read, in order, from ``cu_seq_lens_q/k`` + ``max_length_q/k``
-    kwargs, from restarting ``position_ids`` (B == 1), or from a 2-D padding
-    ``attention_mask`` (rows are unpadded); otherwise every batch row is one
+    kwargs, from a 2-D padding ``attention_mask`` (rows are unpadded), or from
+    restarting ``position_ids`` (B == 1); otherwise every batch row is one
     sequence.  Unknown kwargs (e.g. the collator's raw ``questions``) are
     ignored.
     """
@@ -390,48 +584,14 @@ def siq_varlen_attention_forward(module: torch.nn.Module, query: torch.Tensor, k
         raise ValueError("sliding-window attention is not supported")
     if is_causal is None:
         is_causal = bool(getattr(module, "is_causal", False))
-    bsz, hq, s_q, d = query.shape
-    hkv, s_k = key.shape[1], key.shape[2]
+    d = query.shape[-1]
     if scaling is None:
         scaling = d**-0.5
     target = query.dtype if query.dtype == torch.bfloat16 else torch.bfloat16
     q = query.transpose(1, 2).to(target)
     k = key.transpose(1, 2).to(target)
     v = value.transpose(1, 2).to(target)
-
-    cu_q = kwargs.get("cu_seq_lens_q")
-    cu_k = kwargs.get("cu_seq_lens_k")
-    max_q = kwargs.get("max_length_q")
-    max_k = kwargs.get("max_length_k")
-    position_ids = kwargs.get("position_ids")
-    if cu_q is not None and cu_k is not None and max_q is not None and max_k is not None:
-        out = flash_attn_varlen_func(q.reshape(-1, hq, d), k.reshape(-1, hkv, d), v.reshape(-1, hkv, d),
-                                     cu_q.to(torch.int32), cu_k.to(torch.int32), int(max_q), int(max_k),
-                                     softmax_scale=scaling, causal=is_causal)
-        out = out.reshape(bsz, s_q, hq, d)
-    elif attention_mask is not None and attention_mask.dim() == 2:
-        cu, idx, maxlen = _unpad_from_mask(attention_mask, s_k)
-        if s_q != s_k:
-            raise ValueError("padded (unpacked) inputs need equal query and key lengths")
-        qu = q.reshape(-1, hq, d).index_select(0, idx)
-        ku = k.reshape(-1, hkv, d).index_select(0, idx)
-        vu = v.reshape(-1, hkv, d).index_select(0, idx)
-        ou = flash_attn_varlen_func(qu, ku, vu, cu, cu, maxlen, maxlen, softmax_scale=scaling, causal=is_causal)
-        out = torch.zeros((bsz * s_q, hq, d), dtype=ou.dtype, device=ou.device)
-        out = out.index_copy(0, idx, ou).reshape(bsz, s_q, hq, d)
-    elif position_ids is not None and bsz == 1 and s_q == s_k:
-        cu, maxlen = _cu_from_position_ids(position_ids)
-        out = flash_attn_varlen_func(q.reshape(-1, hq, d), k.reshape(-1, hkv, d), v.reshape(-1, hkv, d), cu, cu,
-                                     maxlen, maxlen, softmax_scale=scaling, causal=is_causal)
-        out = out.reshape(bsz, s_q, hq, d)
-    else:
-        if attention_mask is not None:
-            raise ValueError("siq_varlen expects a 2-D padding mask or None (register its mask interface)")
-        cu_q = torch.arange(0, (bsz + 1) * s_q, s_q, dtype=torch.int32, device=query.device)
-        cu_k = torch.arange(0, (bsz + 1) * s_k, s_k, dtype=torch.int32, device=query.device)
-        out = flash_attn_varlen_func(q.reshape(-1, hq, d), k.reshape(-1, hkv, d), v.reshape(-1, hkv, d), cu_q, cu_k,
-                                     s_q, s_k, softmax_scale=scaling, causal=is_causal)
-        out = out.reshape(bsz, s_q, hq, d)
+    out = _attend_packed(q, k, v, attention_mask, is_causal, scaling, kwargs)
     return out.to(query.dtype).contiguous(), None
 
 
@@ -466,6 +626,9 @@ def attention_flops(cu_seqlens: torch.Tensor, hq: int, d: int, causal: bool, bac
 
 __all__ = [
     "ATTN_IMPLEMENTATION",
+    "flash_attn_varlen_rope_func",
+    "varlen_attn_rope_bwd",
+    "varlen_attn_rope_fwd",
     "AttnPlan",
     "build_attn_plan",
     "cached_attn_plan",

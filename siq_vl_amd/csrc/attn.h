@@ -96,6 +96,16 @@ struct AttnParams {
   const SplitTile* splits;   // [kMaxSplitTiles] split tiles
   const int* nsplit;         // number of split tiles
   PlanHeader* plan;          // the plan these lists belong to
+  // Rotary embedding of q inside the kernels (rcos != nullptr): cos / sin rows
+  // per token ([total_q, D] bf16, D contiguous, token strides rc_tok /
+  // rs_tok).  The forward reads q before rotation, rotates it in registers and
+  // writes the rotated rows to qe (for the backward); the dQ kernel reads the
+  // rotated q and writes dq through the rotation's backward.
+  const bf16* rcos;
+  const bf16* rsin;
+  int64_t rc_tok, rs_tok;
+  bf16* qe;
+  int64_t qe_tok, qe_head;
   int batch, hq, hkv, n_rep;
   int64_t q_tok, q_head, k_tok, k_head, v_tok, v_head, o_tok, o_head;
   int64_t do_tok, do_head, dq_tok, dq_head, dk_tok, dk_head, dv_tok, dv_head;

@@ -29,6 +29,10 @@
 //    scheduler's piece length run as several work items writing fp32 sums to
 //    workspace slots,
 //  * which the partial-sum kernel adds in piece order afterwards.
+// With the rotary embedding fused, the dQ kernel reads the rotated q the
+// forward wrote and stores dq through the rotation's backward (the separate
+// RoPE backward pass's exact roundings); dK stays the gradient of the rotated
+// k, for a k-only RoPE backward pass.
 #include "attn.h"
 
 namespace siq {
@@ -367,7 +371,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_sum_kernel(const AttnParams 
   }
 }
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool ROPE>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p) {
   constexpr int BM = kFwdBM, BN = kFwdBN, NT = 256, NW = NT / 64;
   static_assert(BM == 128 && BN == 64, "128 q rows (4 x 32) by 64 kv rows (2 x 32) per step");
@@ -436,6 +440,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
     lse2 = qvalid ? l2 : INFINITY;
     dlt = qvalid ? acc : 0.f;
   }
+
   f32x16 dq[NDT];
 #pragma unroll
   for (int i = 0; i < NDT; ++i) dq[i] = zero16();
@@ -528,15 +533,50 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
   }
 
   if (qvalid) {
-    bf16* dqp = p.dq + (int64_t)(si.q_start + qrow) * p.dq_tok + (int64_t)hqi * p.dq_head;
+    const int64_t r = si.q_start + qrow;
+    bf16* dqp = p.dq + r * p.dq_tok + (int64_t)hqi * p.dq_head;
+    if constexpr (!ROPE) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
+      for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        bf16x8 a;
+        for (int j = 0; j < 2; ++j) {
+          bf16x8 a;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) a[i] = (bf16)(dq[dt][8 * j + i] * p.scale);
-        st_bf16x8(dqp + 32 * dt + 16 * j + 8 * h, a);
+          for (int i = 0; i < 8; ++i) a[i] = (bf16)(dq[dt][8 * j + i] * p.scale);
+          st_bf16x8(dqp + 32 * dt + 16 * j + 8 * h, a);
+        }
+      }
+    } else {
+      // dq of the q before rotation: the gradient of the rotated q, rounded
+      // to bf16 as the attention's own output would be, through the
+      // rotation's backward.  Lane holds d = 32 dt + 16 j + 8 h + i; the
+      // partner d + D / 2 is d-tile dt + NDT / 2 of the same lane.
+      // (cos / sin held through the kv loop would not fit the registers)
+      const bf16* cp = p.rcos + r * p.rc_tok + 8 * h;
+      const bf16* sp = p.rsin + r * p.rs_tok + 8 * h;
+      bf16x8 rc[D / 16], rs[D / 16];
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) {
+        rc[ks] = ld_bf16x8(cp + 16 * ks);
+        rs[ks] = ld_bf16x8(sp + 16 * ks);
+      }
+#pragma unroll
+      for (int dt = 0; dt < NDT / 2; ++dt) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          bf16x8 g1, g2;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            g1[i] = (bf16)(dq[dt][8 * j + i] * p.scale);
+            g2[i] = (bf16)(dq[dt + NDT / 2][8 * j + i] * p.scale);
+          }
+          // chunk 2 dt + j holds d0 .. d0 + 7 (+ 8 h); the partner is chunk 2 dt + j + D / 32
+          const int d0 = 32 * dt + 16 * j, c0 = 2 * dt + j;
+          bf16x8 o1, o2;
+          rope_bwd8(g1, g2, rc[c0], rc[c0 + D / 32], rs[c0], rs[c0 + D / 32], o1, o2);
+          st_bf16x8(dqp + d0 + 8 * h, o1);
+          st_bf16x8(dqp + d0 + D / 2 + 8 * h, o2);
+        }
       }
     }
   }
@@ -545,7 +585,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
 template <int D, bool CAUSAL>
 hipError_t launch_bwd_t(const AttnParams& p, int qcap, int kvcap, hipStream_t stream) {
   // dQ first: it also writes Delta and LSE2, which the dK/dV kernel reads
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)qcap * p.hq)), dim3(256), 0, stream, p);
+  const dim3 qgrid((unsigned)((int64_t)qcap * p.hq));
+  if (p.rcos != nullptr)
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL, true>), qgrid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL, false>), qgrid, dim3(256), 0, stream, p);
   hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)kvcap * p.hkv)), dim3(512), 0, stream,
                      p);
   hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D>), dim3(min(kMaxSplitTiles * DkvSum<D>::NCH, 512), p.hkv), dim3(256), 0, stream,

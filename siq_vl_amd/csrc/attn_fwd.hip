@@ -24,6 +24,12 @@
 // exceeds it by more than 2^8 (so unnormalised P stays <= 256, exact in the
 // fp32 accumulators and in bf16), and the O rescale is skipped for the whole
 // wave when no row moved -- after the first block it practically never runs.
+//
+// With the rotary embedding fused (ROPE), q arrives before rotation: each lane
+// rotates its Q fragment in registers with the cos / sin rows of its token
+// (the same bf16 roundings as transformers' apply_rotary_pos_emb, so the
+// result is bitwise the separate RoPE pass's) and writes the rotated rows
+// once, for the backward.
 #include "attn.h"
 
 namespace siq {
@@ -32,7 +38,7 @@ namespace {
 
 constexpr float kRescaleLog2 = 8.f;
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool ROPE>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   constexpr int BM = kFwdBM, BN = kFwdBN, NT = 256;
   using Tile = LdsTile<BN, D, NT / 64>;
@@ -71,13 +77,46 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   const bool qvalid = qrow < si.q_len;
   // last kv row this lane's q row may see
   const int lim = CAUSAL ? min(si.k_len - 1, qrow + off) : si.k_len - 1;
+  // The first K / V block goes out before the Q chunks: the loads are
+  // untracked (each block's wait_vmem + barrier orders them), so the wait the
+  // compiler puts before the first use of Q (or, with the rotation, before
+  // rotating it) also covers them, and their latency overlaps Q's.
+  const bf16* kbase = p.k + (int64_t)si.k_start * p.k_tok + (int64_t)hk * p.k_head;
+  const bf16* vbase = p.v + (int64_t)si.k_start * p.v_tok + (int64_t)hk * p.v_head;
+  if (nblk > 0) {
+    kt.template issue<true>(kbase, p.k_tok, si.k_len, smem, wu);
+    vt.template issue<true>(vbase, p.v_tok, si.k_len, smem + TE, wu);
+  }
   bf16x8 qf[D / 16];
   {
-    const bf16* qp = p.q + (int64_t)(si.q_start + (qvalid ? qrow : 0)) * p.q_tok + (int64_t)hqi * p.q_head + 8 * h;
+    const int64_t r = si.q_start + (qvalid ? qrow : 0);
+    const bf16* qp = p.q + r * p.q_tok + (int64_t)hqi * p.q_head + 8 * h;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
       const bf16x8 x = ld_bf16x8(qp + 16 * ks);
       qf[ks] = qvalid ? x : zero_bf16x8();
+    }
+    if constexpr (ROPE) {
+      // lane holds d = 16 ks + 8 h + i; its rotation partner d + D / 2 is chunk ks + HK of the same lane
+      constexpr int HK = D / 32;
+      const bf16* cp = p.rcos + r * p.rc_tok + 8 * h;
+      const bf16* sp = p.rsin + r * p.rs_tok + 8 * h;
+      // every cos / sin chunk in flight with the q chunks before the first use
+      bf16x8 cs[D / 16], sn[D / 16];
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) {
+        cs[ks] = ld_bf16x8(cp + 16 * ks);
+        sn[ks] = ld_bf16x8(sp + 16 * ks);
+      }
+#pragma unroll
+      for (int ks = 0; ks < HK; ++ks) {
+        bf16x8 o1, o2;
+        rope_fwd8(qf[ks], qf[ks + HK], cs[ks], cs[ks + HK], sn[ks], sn[ks + HK], o1, o2);
+        qf[ks] = o1;
+        qf[ks + HK] = o2;
+      }
+      // the rotated rows are stored with the output, after the kv loop: stored
+      // here, every block's wait for its K / V loads would also wait for them
     }
   }
   f32x16 oacc[D / 32];
@@ -85,13 +124,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   for (int i = 0; i < D / 32; ++i) oacc[i] = zero16();
   float mref = -INFINITY, lsum = 0.f;  // reference max (log2 units), per-half partial row sum
 
-  const bf16* kbase = p.k + (int64_t)si.k_start * p.k_tok + (int64_t)hk * p.k_head;
-  const bf16* vbase = p.v + (int64_t)si.k_start * p.v_tok + (int64_t)hk * p.v_head;
-  // K / V loads are untracked: each block's wait_vmem + barrier orders them
-  if (nblk > 0) {
-    kt.template issue<true>(kbase, p.k_tok, si.k_len, smem, wu);
-    vt.template issue<true>(vbase, p.v_tok, si.k_len, smem + TE, wu);
-  }
   wait_vmem();
   __syncthreads();
 
@@ -197,6 +229,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
       p.lse[(int64_t)hqi * p.lse_head + si.q_start + qrow] =
           ltot > 0.f ? (mref + __log2f(ltot)) * kLn2 : -INFINITY;
     }
+    if constexpr (ROPE) {
+      bf16* qe = p.qe + (int64_t)(si.q_start + qrow) * p.qe_tok + (int64_t)hqi * p.qe_head + 8 * h;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) st_bf16x8(qe + 16 * ks, qf[ks]);
+    }
   }
 }
 
@@ -204,7 +241,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
 
 template <int D, bool CAUSAL>
 hipError_t launch_fwd_t(const AttnParams& p, int qcap, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)qcap * p.hq)), dim3(256), 0, stream, p);
+  const dim3 grid((unsigned)((int64_t)qcap * p.hq));
+  if (p.rcos != nullptr)
+    hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, true>), grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, false>), grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

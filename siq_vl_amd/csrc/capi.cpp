@@ -235,11 +235,21 @@ int check_bwd_tensors(const void* q, const void* k, const void* v, const void* o
   return SIQ_OK;
 }
 
-// Forward over a built plan (at plan_base, laid out by L).
+// Forward over a built plan (at plan_base, laid out by L); rope non-null:
+// q is rotated inside the kernel and the rotated rows go to rope->qe.
 int run_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int batch, int64_t total_q,
             int64_t total_k, int hq, int hkv, int d, const int64_t* strides, float scale, int causal,
-            char* plan_base, const PlanLayout& L, hipStream_t s) {
+            char* plan_base, const PlanLayout& L, hipStream_t s, const RopeIn* rope) {
   siq::AttnParams p{};
+  if (rope != nullptr) {
+    p.rcos = static_cast<const siq::bf16*>(rope->cos);
+    p.rsin = static_cast<const siq::bf16*>(rope->sin);
+    p.rc_tok = rope->cos_tok;
+    p.rs_tok = rope->sin_tok;
+    p.qe = static_cast<siq::bf16*>(rope->qe);
+    p.qe_tok = rope->qe_tok;
+    p.qe_head = rope->qe_head;
+  }
   p.q = static_cast<const siq::bf16*>(q);
   p.k = static_cast<const siq::bf16*>(k);
   p.v = static_cast<const siq::bf16*>(v);
@@ -256,9 +266,15 @@ int run_fwd(const void* q, const void* k, const void* v, void* o, float* lse, in
 int run_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout, void* dq,
             void* dk, void* dv, int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
             const int64_t* strides, float scale, int causal, char* plan_base, const PlanLayout& L, char* ws,
-            hipStream_t s) {
+            hipStream_t s, const RopeIn* rope = nullptr) {
   const BwdLayout B = bwd_layout(total_q, hq, d);
   siq::AttnParams p{};
+  if (rope != nullptr) {
+    p.rcos = static_cast<const siq::bf16*>(rope->cos);
+    p.rsin = static_cast<const siq::bf16*>(rope->sin);
+    p.rc_tok = rope->cos_tok;
+    p.rs_tok = rope->sin_tok;
+  }
   p.q = static_cast<const siq::bf16*>(q);
   p.k = static_cast<const siq::bf16*>(k);
   p.v = static_cast<const siq::bf16*>(v);
@@ -299,7 +315,7 @@ int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, fl
   char* base = static_cast<char*>(ws);
   const hipError_t e = build_plan(base, L, cu_q, cu_k, batch, total_q, total_k, hq, hkv, causal != 0, false, s);
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
-  return run_fwd(q, k, v, o, lse, batch, total_q, total_k, hq, hkv, d, strides, scale, causal, base, L, s);
+  return run_fwd(q, k, v, o, lse, batch, total_q, total_k, hq, hkv, d, strides, scale, causal, base, L, s, nullptr);
 }
 
 int siq_attn_varlen_fwd_plan(const void* q, const void* k, const void* v, void* o, float* lse, int batch,
@@ -313,7 +329,7 @@ int siq_attn_varlen_fwd_plan(const void* q, const void* k, const void* v, void* 
   if (plan == nullptr || plan_bytes < L.total || !aligned16(plan))
     return fail(SIQ_ERR_WORKSPACE, "plan needs %zu bytes (16-byte aligned), got %zu", L.total, plan_bytes);
   return run_fwd(q, k, v, o, lse, batch, total_q, total_k, hq, hkv, d, strides, scale, causal,
-                 static_cast<char*>(const_cast<void*>(plan)), L, static_cast<hipStream_t>(stream));
+                 static_cast<char*>(const_cast<void*>(plan)), L, static_cast<hipStream_t>(stream), nullptr);
 }
 
 int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
@@ -354,6 +370,66 @@ int siq_attn_varlen_bwd_plan(const void* q, const void* k, const void* v, const 
   return run_bwd(q, k, v, o, lse, dout, dq, dk, dv, batch, total_q, total_k, hq, hkv, d, strides, scale, causal,
                  static_cast<char*>(const_cast<void*>(plan)), L, static_cast<char*>(ws),
                  static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+namespace {
+
+// cos / sin rows per token: 16-byte aligned, token strides multiples of 8
+// elements (rows are D contiguous bf16).
+int check_rope_rows(const void* cos, const void* sin, int64_t cos_tok, int64_t sin_tok, int64_t total_q) {
+  if (total_q == 0) return SIQ_OK;
+  if (cos == nullptr || sin == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "cos and sin must not be NULL");
+  if (!aligned16(cos) || !aligned16(sin)) return fail(SIQ_ERR_ALIGNMENT, "cos / sin not 16-byte aligned");
+  if (cos_tok < 0 || sin_tok < 0 || (cos_tok & 7) || (sin_tok & 7))
+    return fail(SIQ_ERR_ALIGNMENT, "cos / sin token strides (%lld, %lld) must be non-negative multiples of 8",
+                (long long)cos_tok, (long long)sin_tok);
+  return SIQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int siq_attn_rope_fwd_plan(const void* q, const void* k, const void* v, void* o, float* lse, void* q_embed,
+                           const void* cos, const void* sin, int batch, int64_t total_q, int64_t total_k, int hq,
+                           int hkv, int d, const int64_t* strides, float scale, int causal, const void* plan,
+                           size_t plan_bytes, void* stream) {
+  int rc = check_attn_common(batch, 0, 0, total_q, total_k, hq, hkv, d, scale);
+  if (rc) return rc;
+  if ((rc = check_fwd_tensors(q, k, v, o, lse, total_q, total_k, strides))) return rc;
+  if ((rc = check_tensor("q_embed", q_embed, strides + 8, total_q > 0))) return rc;
+  if ((rc = check_rope_rows(cos, sin, strides[10], strides[11], total_q))) return rc;
+  if (batch == 0 || total_q == 0) return ok();
+  const PlanLayout L = plan_layout(batch, total_q, total_k, true);
+  if (plan == nullptr || plan_bytes < L.total || !aligned16(plan))
+    return fail(SIQ_ERR_WORKSPACE, "plan needs %zu bytes (16-byte aligned), got %zu", L.total, plan_bytes);
+  const RopeIn rope{cos, sin, strides[10], strides[11], q_embed, strides[8], strides[9]};
+  return run_fwd(q, k, v, o, lse, batch, total_q, total_k, hq, hkv, d, strides, scale, causal,
+                 static_cast<char*>(const_cast<void*>(plan)), L, static_cast<hipStream_t>(stream), &rope);
+}
+
+int siq_attn_rope_bwd_plan(const void* q_embed, const void* k, const void* v, const void* o, const float* lse,
+                           const void* dout, void* dq, void* dk, void* dv, const void* cos, const void* sin, int batch,
+                           int64_t total_q, int64_t total_k, int hq, int hkv, int d, const int64_t* strides,
+                           float scale, int causal, const void* plan, size_t plan_bytes, void* ws, size_t ws_bytes,
+                           void* stream) {
+  int rc = check_attn_common(batch, 0, 0, total_q, total_k, hq, hkv, d, scale);
+  if (rc) return rc;
+  if ((rc = check_bwd_tensors(q_embed, k, v, o, lse, dout, dq, dk, dv, total_q, total_k, strides))) return rc;
+  if ((rc = check_rope_rows(cos, sin, strides[16], strides[17], total_q))) return rc;
+  if (batch == 0 || (total_q == 0 && total_k == 0)) return ok();
+  const PlanLayout L = plan_layout(batch, total_q, total_k, true);
+  if (plan == nullptr || plan_bytes < L.total || !aligned16(plan))
+    return fail(SIQ_ERR_WORKSPACE, "plan needs %zu bytes (16-byte aligned), got %zu", L.total, plan_bytes);
+  const size_t need = bwd_layout(total_q, hq, d).total;
+  if (ws == nullptr || ws_bytes < need || !aligned16(ws))
+    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
+  const RopeIn rope{cos, sin, strides[16], strides[17], nullptr, 0, 0};
+  return run_bwd(q_embed, k, v, o, lse, dout, dq, dk, dv, batch, total_q, total_k, hq, hkv, d, strides, scale,
+                 causal, static_cast<char*>(const_cast<void*>(plan)), L, static_cast<char*>(ws),
+                 static_cast<hipStream_t>(stream), &rope);
 }
 
 size_t siq_flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk_tokens, int need_dweight) {
@@ -453,8 +529,9 @@ int rope_call(bool backward, const void* x0, const void* x1, const void* cosp, c
   const char* nm[6] = {backward ? "dq_embed" : "q", backward ? "dk_embed" : "k", "cos", "sin",
                        backward ? "dq" : "q_embed", backward ? "dk" : "k_embed"};
   if (batch < 0 || seqlen < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "batch and seqlen must be >= 0");
-  if (hq <= 0 || hkv <= 0 || hq > 4096 || hkv > 4096)
-    return fail(SIQ_ERR_INVALID_ARGUMENT, "head counts must be in [1, 4096] (hq=%d, hkv=%d)", hq, hkv);
+  if (hq < 0 || hkv <= 0 || hq > 4096 || hkv > 4096)
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "head counts must be hq in [0, 4096], hkv in [1, 4096] (hq=%d, hkv=%d)",
+                hq, hkv);
   if (d < 16 || d > 512 || d % 16 != 0)
     return fail(SIQ_ERR_UNSUPPORTED, "head_dim %d unsupported (a multiple of 16 in [16, 512])", d);
   if (st == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "strides must not be NULL");
@@ -464,6 +541,7 @@ int rope_call(bool backward, const void* x0, const void* x1, const void* cosp, c
   const void* ptr[6] = {x0, x1, cosp, sinp, y0, y1};
   const int first[6] = {0, 3, 6, 8, 10, 13}, count[6] = {3, 3, 2, 2, 3, 3};
   for (int t = 0; t < 6; ++t) {
+    if (hq == 0 && (t == 0 || t == 4)) continue;  // k-only pass: q and its output are not touched
     if (ptr[t] == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "%s must not be NULL", nm[t]);
     if (!aligned16(ptr[t])) return fail(SIQ_ERR_ALIGNMENT, "%s is not 16-byte aligned", nm[t]);
     for (int j = 0; j < count[t]; ++j) {

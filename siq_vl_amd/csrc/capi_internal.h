@@ -28,8 +28,18 @@ int check_attn_common(int batch, int max_q, int max_k, int64_t total_q, int64_t 
 int check_cu(int batch, const void* cu_q, const void* cu_k);
 int check_fwd_tensors(const void* q, const void* k, const void* v, void* o, float* lse, int64_t total_q,
                       int64_t total_k, const int64_t* strides);
+// The rotary embedding fused into the attention kernels: cos / sin rows per
+// token, and (forward) where the rotated q rows go.
+struct RopeIn {
+  const void* cos;
+  const void* sin;
+  int64_t cos_tok, sin_tok;
+  void* qe;
+  int64_t qe_tok, qe_head;
+};
+
 int run_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int batch, int64_t total_q,
             int64_t total_k, int hq, int hkv, int d, const int64_t* strides, float scale, int causal,
-            char* plan_base, const PlanLayout& L, hipStream_t s);
+            char* plan_base, const PlanLayout& L, hipStream_t s, const RopeIn* rope);
 
 }  // namespace siq_capi

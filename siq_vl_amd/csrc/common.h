@@ -83,6 +83,43 @@ __device__ __forceinline__ void transpose4x8(const u32x4 (&rows)[4], u32x2 (&col
   }
 }
 
+// fp32 -> nearest-even bf16 -> fp32.  Used where a result must repeat a bf16
+// torch op's rounding exactly.  The empty asm makes x opaque: the compiler
+// otherwise treats (float)(bf16)(a * b) of two bf16 values as a bf16 multiply
+// that it may fuse, unrounded, into a following add (v_fmac_f32).  The
+// conversion itself is gfx950's v_cvt_pk_bf16_f32 (round to nearest even, as
+// torch rounds).
+__device__ __forceinline__ float rbf(float x) {
+  asm("" : "+v"(x));
+  return (float)(bf16)x;
+}
+
+// Rotary embedding of one 8-element chunk pair (x1 at d, x2 at d + D/2), as
+// transformers' apply_rotary_pos_emb evaluates it on bf16 tensors
+// (modeling_qwen2.py:105-135: q * cos + rotate_half(q) * sin, each op rounded):
+//   o1 = rb(rb(x1 c1) + rb(-x2 s1)),  o2 = rb(rb(x2 c2) + rb(x1 s2)).
+__device__ __forceinline__ void rope_fwd8(const bf16x8& x1, const bf16x8& x2, const bf16x8& c1, const bf16x8& c2,
+                                          const bf16x8& s1, const bf16x8& s2, bf16x8& o1, bf16x8& o2) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float u = (float)x1[k], v = (float)x2[k];
+    o1[k] = (bf16)(rbf(u * (float)c1[k]) + rbf(-v * (float)s1[k]));
+    o2[k] = (bf16)(rbf(v * (float)c2[k]) + rbf(u * (float)s2[k]));
+  }
+}
+
+// Its autograd backward on the bf16 upstream gradients g1 (at d), g2 (at d + D/2):
+//   dx1 = rb(rb(g1 c1) + rb(g2 s2)),  dx2 = rb(rb(g2 c2) - rb(g1 s1)).
+__device__ __forceinline__ void rope_bwd8(const bf16x8& g1, const bf16x8& g2, const bf16x8& c1, const bf16x8& c2,
+                                          const bf16x8& s1, const bf16x8& s2, bf16x8& o1, bf16x8& o2) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float u = (float)g1[k], v = (float)g2[k];
+    o1[k] = (bf16)(rbf(u * (float)c1[k]) + rbf(v * (float)s2[k]));
+    o2[k] = (bf16)(rbf(v * (float)c2[k]) - rbf(u * (float)s1[k]));
+  }
+}
+
 __device__ __forceinline__ float wave_max_xor32(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 __device__ __forceinline__ float wave_sum_xor32(float x) { return x + __shfl_xor(x, 32); }
 

@@ -70,5 +70,5 @@ extern "C" int siq_attn_varlen_fwd_noalloc(const void* q, const void* k, const v
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = build_plan(base, L, cu_q, cu_k, batch, total_q, total_k, hq, hkv, causal != 0, false, s);
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
-  return run_fwd(q, k, v, o, lse, batch, total_q, total_k, hq, hkv, d, strides, scale, causal, base, L, s);
+  return run_fwd(q, k, v, o, lse, batch, total_q, total_k, hq, hkv, d, strides, scale, causal, base, L, s, nullptr);
 }

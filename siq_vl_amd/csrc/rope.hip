@@ -21,6 +21,9 @@
 // HBM-bound, 2 * (Hq + Hkv) * D * 2 bytes per token plus the cos / sin rows
 // (L2 hits after the first head of a token).
 //
+// hq may be 0 (a k-only pass, for the attention kernels that rotate q
+// themselves).
+//
 // Work split: a thread owns one 8-element chunk c of the first half (and the
 // matching chunk of the second) of one token at a time: D / 16 threads per
 // token, 256 / (D / 16) tokens per block step, blocks striding over tokens
@@ -35,32 +38,15 @@ namespace siq {
 
 namespace {
 
-// fp32 -> nearest-even bf16 -> fp32, in integer arithmetic.  Written out
-// because the compiler treats (float)(bf16)(a * b) of two bf16 values as a
-// bf16 multiply it may then fuse, unrounded, into the following add
-// (v_fmac_f32), which would break the reference's rounding.
-__device__ __forceinline__ float rbf(float x) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
-  const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
-  return x != x ? x : __builtin_bit_cast(float, r);
-}
-
 template <bool BWD>
 __device__ __forceinline__ void rope_row(const bf16* src, bf16* dst, int half, const bf16x8& c1, const bf16x8& c2,
                                          const bf16x8& s1, const bf16x8& s2) {
   const bf16x8 x1 = ld_bf16x8(src), x2 = ld_bf16x8(src + half);
   bf16x8 o1, o2;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const float u = (float)x1[k], v = (float)x2[k];
-    if (!BWD) {
-      o1[k] = (bf16)(rbf(u * (float)c1[k]) + rbf(-v * (float)s1[k]));
-      o2[k] = (bf16)(rbf(v * (float)c2[k]) + rbf(u * (float)s2[k]));
-    } else {
-      o1[k] = (bf16)(rbf(u * (float)c1[k]) + rbf(v * (float)s2[k]));
-      o2[k] = (bf16)(rbf(v * (float)c2[k]) - rbf(u * (float)s1[k]));
-    }
-  }
+  if (!BWD)
+    rope_fwd8(x1, x2, c1, c2, s1, s2, o1, o2);
+  else
+    rope_bwd8(x1, x2, c1, c2, s1, s2, o1, o2);
   st_bf16x8(dst, o1);
   st_bf16x8(dst + half, o2);
 }

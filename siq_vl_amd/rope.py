@@ -19,6 +19,10 @@ Layers:
 * ``enable_fused_rope()`` -- installs it as
   ``transformers.models.qwen2.modeling_qwen2.apply_rotary_pos_emb``, the name
   ``Qwen2Attention.forward`` looks up at call time.
+* ``enable_fused_rope_attention(model)`` -- goes one step further on a model
+  using the ``siq_varlen`` attention backend: rotation and attention become
+  one op (``flash_attn_varlen_rope_func``) whose backward rotates dq inside
+  the dQ kernel, leaving a k-only rotation pass; bitwise the same results.
 """
 
 from __future__ import annotations
@@ -150,6 +154,104 @@ def disable_fused_rope() -> None:
     if _ORIGINAL is not None and m.apply_rotary_pos_emb is apply_rotary_pos_emb:
         m.apply_rotary_pos_emb = _ORIGINAL
     _ORIGINAL = None
+
+
+# --------------------------------------------------------------------------- rotation fused into attention
+def _launch_k(fn_name: str, x1, cos, sin, y1) -> None:
+    """k-only pass (hq = 0): q and its output are not touched."""
+    b, s, hkv, d = x1.shape
+    strides = [0, 0, 0, *x1.stride()[:3], *cos.stride()[:2], *sin.stride()[:2], 0, 0, 0, *y1.stride()[:3]]
+    stream = torch.cuda.current_stream(x1.device).cuda_stream
+    rc = getattr(_lib.lib(), fn_name)(None, x1.data_ptr(), cos.data_ptr(), sin.data_ptr(), None, y1.data_ptr(), b, s,
+                                      0, hkv, d, _lib.int64_array(strides), stream)
+    _lib.check(rc, fn_name)
+
+
+def _k_only(fn_name: str, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    _check(k, k, cos, sin)
+    k = _prep(k, 4)
+    cos, sin = _prep(_expand_cs(cos, k.shape[0]), 3), _prep(_expand_cs(sin, k.shape[0]), 3)
+    out = torch.empty_like(k)
+    if k.numel():
+        _launch_k(fn_name, k, cos, sin, out)
+    return out
+
+
+class _RopeK(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, k, cos, sin):
+        ctx.save_for_backward(cos, sin)
+        return _k_only("siq_rope_fwd", k, cos, sin)
+
+    @staticmethod
+    def backward(ctx, dke):
+        cos, sin = ctx.saved_tensors
+        return _k_only("siq_rope_bwd", dke, cos, sin), None, None
+
+
+def rotate_k_backward(dk_embed: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """The rotation's backward for k alone on token-major ``[T, Hkv, D]`` with
+    ``cos`` / ``sin [T, D]`` (one k-only pass of ``siq_rope_bwd``)."""
+    return _k_only("siq_rope_bwd", dk_embed[None], cos[None], sin[None])[0]
+
+
+def rotate_k(k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """k half of ``apply_rotary_pos_emb`` on ``[B, S, Hkv, D]`` (autograd-aware,
+    bitwise ``rope_fwd``'s k_embed); the q half is done inside the attention
+    kernels by ``flash_attn_varlen_rope_func``."""
+    if cos.requires_grad or sin.requires_grad:
+        raise ValueError("gradients with respect to cos / sin are not supported")
+    return _RopeK.apply(k, cos, sin)
+
+
+def fused_qwen2_attention_forward(self, hidden_states: torch.Tensor, position_embeddings, attention_mask,
+                                  past_key_values=None, **kwargs):
+    """``Qwen2Attention.forward`` (transformers models/qwen2/modeling_qwen2.py:
+    176-234; the reference's decoder attention via SiQ_VLTextModel,
+    siq_vl/model/modeling.py:139-153) with the rotary embedding and the
+    attention as one op (``flash_attn_varlen_rope_func``): the rotation's
+    backward of q runs inside the attention backward's dQ kernel.  Same
+    signature and return; bitwise the outputs and gradients of the unfused
+    path (``enable_fused_rope`` + ``siq_varlen``).  Calls it cannot serve (a
+    KV cache, another attention backend, non-bf16 or CPU tensors) take the
+    stock forward."""
+    from .attention import ATTN_IMPLEMENTATION, _attend_packed
+
+    cos, sin = position_embeddings
+    usable = (past_key_values is None and getattr(self.config, "_attn_implementation", None) == ATTN_IMPLEMENTATION
+              and hidden_states.is_cuda and hidden_states.dtype == torch.bfloat16
+              and cos.dtype == torch.bfloat16 and sin.dtype == torch.bfloat16
+              and getattr(self, "sliding_window", None) is None and self.head_dim in (64, 128))
+    if not usable:
+        return type(self).forward(self, hidden_states, position_embeddings, attention_mask,
+                                  past_key_values=past_key_values, **kwargs)
+    dropout = 0.0 if not self.training else self.attention_dropout
+    if dropout:
+        raise ValueError("siq_varlen attention does not implement dropout")
+    input_shape = hidden_states.shape[:-1]
+    hidden_shape = (*input_shape, -1, self.head_dim)
+    q = self.q_proj(hidden_states).view(hidden_shape)  # [B, S, Hq, D]: the token-major layout the kernels read
+    k = self.k_proj(hidden_states).view(hidden_shape)
+    v = self.v_proj(hidden_states).view(hidden_shape)
+    out = _attend_packed(q, k, v, attention_mask, bool(self.is_causal), self.scaling, kwargs, rope=(cos, sin))
+    attn_output = out.reshape(*input_shape, -1).contiguous()
+    return self.o_proj(attn_output), None
+
+
+def enable_fused_rope_attention(model: torch.nn.Module) -> int:
+    """Installs ``fused_qwen2_attention_forward`` on every Qwen2 attention
+    layer of ``model`` (the model must use ``attn_implementation="siq_varlen"``
+    for the fusion to apply); returns the number of layers patched."""
+    import types
+
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention
+
+    n = 0
+    for mod in model.modules():
+        if isinstance(mod, Qwen2Attention):
+            mod.forward = types.MethodType(fused_qwen2_attention_forward, mod)
+            n += 1
+    return n
 
 
 def rope_bytes(tokens: int, hq: int, hkv: int, d: int) -> int:

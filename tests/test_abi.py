@@ -248,8 +248,9 @@ def _rope(lib, fwd=True, **kw):
     (dict(d=72), _lib.SIQ_ERR_UNSUPPORTED),
     (dict(d=0), _lib.SIQ_ERR_UNSUPPORTED),
     (dict(d=1024), _lib.SIQ_ERR_UNSUPPORTED),
-    (dict(hq=0), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(hq=-1), _lib.SIQ_ERR_INVALID_ARGUMENT),
     (dict(hkv=-1), _lib.SIQ_ERR_INVALID_ARGUMENT),
+    (dict(hkv=0), _lib.SIQ_ERR_INVALID_ARGUMENT),
     (dict(hq=5000), _lib.SIQ_ERR_INVALID_ARGUMENT),
     (dict(batch=1 << 20, seqlen=1 << 12), _lib.SIQ_ERR_INVALID_ARGUMENT),
     (dict(batch=-1), _lib.SIQ_ERR_INVALID_ARGUMENT),
@@ -272,6 +273,37 @@ def test_rope_odd_strides_rejected(lib, pos):
     assert _rope(lib, strides=_lib.int64_array(st)) == _lib.SIQ_ERR_ALIGNMENT
     st[pos] = -128
     assert _rope(lib, strides=_lib.int64_array(st)) == _lib.SIQ_ERR_ALIGNMENT
+
+
+def test_rope_k_only_pass_validation(lib):
+    # hq = 0: q and its output are not read (may be NULL); k, cos, sin and k's output still are
+    assert _rope(lib, hq=0, x0=None, y0=None, seqlen=0) == _lib.SIQ_OK
+    assert _rope(lib, hq=0, x0=None, y0=None, x1=None) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    assert _rope(lib, False, hq=0, x0=None, y0=None, y1=FAKE + 8) == _lib.SIQ_ERR_ALIGNMENT
+
+
+def test_rope_attention_entry_validation(lib):
+    need = lib.siq_attn_plan_bytes(2, 16, 16)
+    f = lib.siq_attn_rope_fwd_plan
+    st = _strides(12)
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, 2, 16, 16, 4, 2, 128, st, 0.1, 1, FAKE, need,
+             None) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE + 8, FAKE, 2, 16, 16, 4, 2, 128, st, 0.1, 1, FAKE, need,
+             None) == _lib.SIQ_ERR_ALIGNMENT
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, 2, 16, 16, 4, 2, 128, st, 0.1, 1, FAKE, need,
+             None) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    bad = [128] * 12
+    bad[10] = 132
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, _lib.int64_array(bad), 0.1, 1, FAKE,
+             need, None) == _lib.SIQ_ERR_ALIGNMENT
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, st, 0.1, 1, FAKE, need - 16,
+             None) == _lib.SIQ_ERR_WORKSPACE
+    b = lib.siq_attn_rope_bwd_plan
+    own = lib.siq_attn_bwd_plan_workspace_bytes(2, 16, 16, 4, 2, 128)
+    assert b(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, 2, 16, 16, 4, 2, 128, _strides(18),
+             0.1, 1, FAKE, need, FAKE, own, None) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    assert b(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, _strides(18),
+             0.1, 1, FAKE, need, FAKE, own - 16, None) == _lib.SIQ_ERR_WORKSPACE
 
 
 def test_rope_empty_is_a_no_op(lib):
