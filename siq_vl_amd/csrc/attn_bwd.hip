@@ -71,8 +71,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
   bf16* Ks = smem + NS * STAGE;
   bf16* Vs = Ks + KVTile::ELEMS;
 
-  // 1-D grid over (item, kv-head), kv-head fastest, runs of 32 per XCD
-  const int e = xcd_order(blockIdx.x, gridDim.x, 32);
+  // 1-D grid over (item, kv-head), kv-head fastest; each XCD takes one item
+  // (all its kv-heads) per run, so the heaviest-first items go round the XCDs
+  const int e = xcd_order(blockIdx.x, gridDim.x, p.hkv);
   const int ii = e / p.hkv, hk = e - ii * p.hkv;
   const KvItem it = p.kvitems[ii];
   // every field loaded before the idle test (the compiler would otherwise
@@ -391,10 +392,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
   tr.init(lane);
   const float c = p.scale_log2;
 
-  // 1-D grid over (q tile, q-head), q-head fastest: the heads that share a
-  // kv-head read the same K / V blocks; each XCD gets runs of about 64
-  // entries (its resident workgroups), whole tiles at a time
-  const int e = xcd_order(blockIdx.x, gridDim.x, p.hq * max(1, 64 / p.hq));
+  // 1-D grid over (q tile, q-head), q-head fastest; each XCD takes whole
+  // tiles, one per run, so the heaviest-first tiles go round the XCDs
+  const int e = xcd_order(blockIdx.x, gridDim.x, p.hq);
   const int ti = e / p.hq, hqi = e - ti * p.hq, hk = hqi / p.n_rep;
   const QTile tl = p.qtiles[ti];
   // every field loaded before the idle test (the compiler would otherwise

@@ -57,9 +57,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   const float c = p.scale_log2;
 
   // 1-D grid over (q tile, q-head), q-head fastest: the heads that share a
-  // kv-head read the same K / V blocks; each XCD gets runs of about 64
-  // entries (its resident workgroups), whole tiles at a time
-  const int e = xcd_order(blockIdx.x, gridDim.x, p.hq * max(1, 64 / p.hq));
+  // kv-head read the same K / V blocks, so each XCD takes whole tiles (runs
+  // of hq entries, sharing K / V through its L2) -- and only one tile per
+  // run, so that the heaviest-first tiles are dealt out over the XCDs in
+  // turn (longer runs hand the first XCD the heaviest tiles of every round)
+  const int e = xcd_order(blockIdx.x, gridDim.x, p.hq);
   const int ti = e / p.hq, hqi = e - ti * p.hq, hk = hqi / p.n_rep;
   const QTile tl = p.qtiles[ti];
   // every field loaded before the idle test (the compiler would otherwise
