@@ -249,24 +249,26 @@ struct DhArgs {
   int nI, nJ, splits;
 };
 
-// dH tiles: block b runs on XCD x = b % 8, which takes token tiles x, x + 8,
-// ... in turn, each with its nI hdim tiles (consecutive blocks there, sharing
-// the dZ slab through the XCD's L2).  Token tiles past the valid rows are
-// empty, so striding them over the XCDs keeps every XCD equally loaded
-// (a contiguous run per XCD would leave the last XCDs idle).  The grid is
-// 8 nI ceil(nJ / 8) blocks.
-__device__ __forceinline__ bool dh_tile_of(int nI, int nJ, int& ti, int& tj) {
+// dH work: a unit is one (token tile, vocab split); its nI hdim tiles share
+// the unit's dZ slab, so they run as consecutive blocks on one XCD (block b
+// runs on XCD b % 8).  Units are dealt out over the XCDs in turn, splits of a
+// token tile on different XCDs: every XCD gets the same number of units, also
+// when the token tiles past the valid rows (which return at once) are many --
+// a whole token tile per XCD left some XCDs half as loaded as others.  The
+// grid is 8 nI ceil(nJ splits / 8) blocks.
+__device__ __forceinline__ bool dh_tile_of(int nI, int nJ, int splits, int& ti, int& tj, int& split) {
   const int x = (int)(blockIdx.x % kXcds), k = (int)(blockIdx.x / kXcds);
   ti = k % nI;
-  tj = x + kXcds * (k / nI);
+  const int unit = x + kXcds * (k / nI);
+  tj = unit / splits;
+  split = unit - tj * splits;
   return tj < nJ;
 }
 
 __global__ __launch_bounds__(NT) void flce_dh_kernel(const DhArgs p) {
   __shared__ __align__(16) bf16 smem[4 * SLAB];
-  int ti, tj;
-  if (!dh_tile_of(p.nI, p.nJ, ti, tj)) return;
-  const int split = blockIdx.y;
+  int ti, tj, split;
+  if (!dh_tile_of(p.nI, p.nJ, p.splits, ti, tj, split)) return;
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
   const int64_t nv = *p.nvalid - p.c0;
   if (j0 >= nv) return;
@@ -716,8 +718,9 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
     dh.nI = (int)((Hd + BI - 1) / BI);
     dh.nJ = (int)((nc + BJ - 1) / BJ);
     {
-      const int grid = kXcds * dh.nI * ((dh.nJ + kXcds - 1) / kXcds);
-      hipLaunchKernelGGL(flce_dh_kernel, dim3(grid, (unsigned)L.splits), dim3(NT), 0, stream, dh);
+      const int units = dh.nJ * (int)L.splits;
+      const int grid = kXcds * dh.nI * ((units + kXcds - 1) / kXcds);
+      hipLaunchKernelGGL(flce_dh_kernel, dim3(grid), dim3(NT), 0, stream, dh);
     }
     if (L.splits > 1) {
       const int64_t nvec = nc * Hd / 8;
