@@ -68,7 +68,7 @@ __global__ __launch_bounds__(NT) void flce_logits_kernel(const LogitsArgs p) {
   const int64_t i0 = (int64_t)ti * BI, j0 = (int64_t)tj * BJ;
   if (j0 >= *p.nvalid - p.c0) return;  // token tile holds no valid row
   f32x16 acc[4][2];
-  gemm_core<true, true>(smem, p.W, p.H, i0, j0, 0, p.W.cols, acc);
+  gemm_core<true, true, true>(smem, p.W, p.H, i0, j0, 0, p.W.cols, acc);
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int wi = w & 1, wj = w >> 1;
@@ -171,12 +171,17 @@ struct RowArgs {
   int rewrite;           // 0: loss only (E was never stored)
 };
 
-// One wave per token row.  lse2 = M + log2(sum_t s_t 2^(m_t - M)); then the
-// row of E becomes dZ = E * f_t - g [v == y], f_t = 2^(m_t - lse2) * g, in
-// fp32 and rounded to bf16 once (zero for an ignored row: g = 0).
-__global__ __launch_bounds__(256) void flce_row_kernel(const RowArgs p) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+// One wave (one workgroup) per token row.  lse2 = M + log2(sum_t s_t
+// 2^(m_t - M)); then the row of E becomes dZ = E * f_t - g [v == y], f_t =
+// 2^(m_t - lse2) * g, in fp32 and rounded to bf16 once (zero for an ignored
+// row: g = 0).  The factors f_t are computed once per tile into LDS, in
+// segments of kRowSegTiles tiles, so the streaming loop does one LDS read and
+// eight multiplies per 16 bytes.
+constexpr int kRowSegTiles = 1024;
+__global__ __launch_bounds__(64) void flce_row_kernel(const RowArgs p) {
+  __shared__ float fsh[kRowSegTiles];
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
   // rows past the last token tile with a valid row are read by no GEMM
   if (row >= p.nc || row >= ((*p.nvalid - p.c0 + BJ - 1) / BJ) * BJ) return;
   const float* m = p.mpart + row * p.nvt;
@@ -197,21 +202,16 @@ __global__ __launch_bounds__(256) void flce_row_kernel(const RowArgs p) {
   if (!p.rewrite) return;
   // dZ, 8 columns per lane per chunk (V is a multiple of 8, so a chunk never
   // straddles the row end; 8 aligned columns never straddle a 256-column
-  // tile).  An ignored row's dZ is zero: written without reading E.
+  // tile: chunk c lies in tile c / 32).  An ignored row's dZ is zero: written
+  // without reading E.
   bf16* e = p.E + row * p.V;
   const int64_t nchunk = p.V / 8;
   if (gv == 0.f) {
     for (int64_t c = lane; c < nchunk; c += 64) st_bf16x8(e + 8 * c, zero_bf16x8());
     return;
   }
-  // U chunks per lane in flight, with their tile maxima: chunk c (columns 8 c ..
-  // 8 c + 7) lies in tile c / 32, so lane chunks c0 + 64 u sit in tiles
-  // c0 / 32 + 2 u, and all 2 U loads of a batch go out before the first use
-  // (a per-chunk load of m would wait once per chunk)
-  constexpr int U = 8;
-  auto chunk = [&](const bf16x8& x, float mt, int64_t c) {
+  auto chunk = [&](const bf16x8& x, float fv, int64_t c) {
     const int64_t v0 = 8 * c;
-    const float fv = exp2f_fast(mt - lse2) * gv;
     bf16x8 o;
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = (bf16)((float)x[i] * fv);
@@ -222,19 +222,27 @@ __global__ __launch_bounds__(256) void flce_row_kernel(const RowArgs p) {
     }
     st_bf16x8(e + v0, o);
   };
-  int64_t c0 = lane;
-  for (; c0 + 64 * (U - 1) < nchunk; c0 += 64 * U) {
-    bf16x8 x[U];
-    float mt[U];
+  // U chunks per lane in flight: lane chunks c + 64 u sit in tiles c / 32 + 2 u
+  // (the pass streams E in and dZ out at the device's mixed read / write rate;
+  // deeper unrolling and non-temporal accesses measured no faster)
+  constexpr int U = 8;
+  for (int64_t t0 = 0; t0 < p.nvt; t0 += kRowSegTiles) {
+    const int nt = (int)min((int64_t)kRowSegTiles, p.nvt - t0);
+    __syncthreads();  // the previous segment's factors are no longer read
+    for (int t = lane; t < nt; t += 64) fsh[t] = exp2f_fast(m[t0 + t] - lse2) * gv;
+    __syncthreads();
+    const int64_t cb = 32 * t0, ce = min(nchunk, 32 * (t0 + nt));
+    int64_t c = cb + lane;
+    for (; c + 64 * (U - 1) < ce; c += 64 * U) {
+      bf16x8 x[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      x[u] = ld_bf16x8(e + 8 * (c0 + 64 * u));
-      mt[u] = m[(c0 >> 5) + 2 * u];
+      for (int u = 0; u < U; ++u) x[u] = ld_bf16x8(e + 8 * (c + 64 * u));
+      const int tb = (int)((c - cb) >> 5);
+#pragma unroll
+      for (int u = 0; u < U; ++u) chunk(x[u], fsh[tb + 2 * u], c + 64 * u);
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) chunk(x[u], mt[u], c0 + 64 * u);
+    for (; c < ce; c += 64) chunk(ld_bf16x8(e + 8 * c), fsh[(c - cb) >> 5], c);
   }
-  for (; c0 < nchunk; c0 += 64) chunk(ld_bf16x8(e + 8 * c0), m[c0 >> 5], c0);
 }
 
 // ---------------------------------------------------------------- dH
@@ -697,7 +705,7 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
     rw.V = V;
     rw.ignore_index = a.ignore_index;
     rw.rewrite = grads ? 1 : 0;
-    hipLaunchKernelGGL(flce_row_kernel, dim3((unsigned)((nc + 3) / 4)), dim3(256), 0, stream, rw);
+    hipLaunchKernelGGL(flce_row_kernel, dim3((unsigned)nc), dim3(64), 0, stream, rw);
     if (!grads) continue;
 
     DhArgs dh{};

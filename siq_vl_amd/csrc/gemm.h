@@ -210,7 +210,15 @@ __device__ __forceinline__ bool tile_of(int nI, int nJ, int GI, int& ti, int& tj
 // LA / LB load the A / B slab of the k-step starting at k0 into an LDS slab:
 // issue(k0, lds, wu), every row / chunk in bounds (OpLoad below for a
 // row-major operand; gathering loaders work the same way).
-template <bool AKC, bool BKC, class LA, class LB>
+//
+// PF: the operand fragments of each k-step are read two 16-wide k-slices
+// ahead of the products that use them (the reads of slice ks + 2 go out right
+// after the products of ks), with scheduling groups pinning that order (the
+// compiler otherwise pulls every read next to its first use and waits on it).
+// It pays where both operands are k-contiguous (six 16-byte reads per slice);
+// with a transposed operand (ten or twelve reads per slice, more than the LDS
+// counter holds two slices of) the plain order is faster.
+template <bool AKC, bool BKC, class LA, class LB, bool PF = false>
 __device__ __forceinline__ void gemm_core_l(bf16* smem, const LA& la, const LB& lb, int64_t kb, int64_t ke,
                                             f32x16 (&acc)[4][2]) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -250,17 +258,46 @@ __device__ __forceinline__ void gemm_core_l(bf16* smem, const LA& la, const LB& 
       la.issue(kn, nx, wu);
       lb.issue(kn, nx + SLAB, wu);
     }
+    if constexpr (PF) {
+      constexpr int KS = BK / 16;
+      constexpr int R = (AKC ? 4 : 8) + (BKC ? 2 : 4);  // LDS read instructions per slice
+      bf16x8 af[KS][4], bfr[KS][2];
+      auto fetch = [&](int ks) {
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 af[4], bfr[2];
+        for (int t = 0; t < 4; ++t) af[ks][t] = ra.read(As, t, ks);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) af[t] = ra.read(As, t, ks);
+        for (int t = 0; t < 2; ++t) bfr[ks][t] = rb.read(Bs, t, ks);
+      };
+      fetch(0);
+      fetch(1);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) bfr[t] = rb.read(Bs, t, ks);
+      for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+        for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) acc[a][b] = mfma32(af[a], bfr[b], acc[a][b]);
+          for (int b = 0; b < 2; ++b) acc[a][b] = mfma32(af[ks][a], bfr[ks][b], acc[a][b]);
+        if (ks + 2 < KS) fetch(ks + 2);
+      }
+      // groups (mask 0x100: LDS reads, 0x008: MFMA): reads of slices 0, 1; products of 0; reads of 2; ...
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * R, 0);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        if (ks + 2 < KS) __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        bf16x8 af[4], bfr[2];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) af[t] = ra.read(As, t, ks);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) bfr[t] = rb.read(Bs, t, ks);
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b) acc[a][b] = mfma32(af[a], bfr[b], acc[a][b]);
+      }
     }
     wait_vmem();
     __syncthreads();
@@ -283,7 +320,7 @@ struct OpLoad {
 };
 
 // gemm_core_l over two row-major operands, tile (i0, j0).
-template <bool AKC, bool BKC>
+template <bool AKC, bool BKC, bool PF = false>
 __device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B, int64_t i0, int64_t j0, int64_t kb,
                                           int64_t ke, f32x16 (&acc)[4][2]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -291,7 +328,7 @@ __device__ __forceinline__ void gemm_core(bf16* smem, const GOp& A, const GOp& B
   OpLoad<BKC> lb;
   la.init(A, i0, lane, w);
   lb.init(B, j0, lane, w);
-  gemm_core_l<AKC, BKC>(smem, la, lb, kb, ke, acc);
+  gemm_core_l<AKC, BKC, OpLoad<AKC>, OpLoad<BKC>, PF>(smem, la, lb, kb, ke, acc);
 }
 
 }  // namespace gemm
