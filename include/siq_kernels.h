@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define SIQ_ABI_VERSION 2
+#define SIQ_ABI_VERSION 3
 
 enum siq_status {
   SIQ_OK = 0,
@@ -88,16 +88,23 @@ int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, fl
 /* Backward of siq_attn_varlen_fwd (the autograd backward of the same call in
  * the reference path).  Inputs q, k, v, o, lse as produced/consumed by the
  * forward, dout like o; outputs dq like q, dk/dv like k/v, each written in full
- * (no accumulation).  Deterministic: no atomics, bitwise reproducible.
+ * (no accumulation).
+ * deterministic != 0: no atomics, bitwise reproducible (dQ in a kernel of its
+ * own that recomputes S and dP).  deterministic == 0: dQ = dS K is formed in
+ * the dK/dV kernel and summed with fp32 atomics in the workspace (the sum
+ * order varies from run to run; the workspace grows by total_q * hq * d * 4
+ * bytes).  flash-attn's flash_attn_varlen_func(deterministic=...) flag.
  * strides[16] = {q_tok, q_head, k_tok, k_head, v_tok, v_head, o_tok, o_head,
  *                do_tok, do_head, dq_tok, dq_head, dk_tok, dk_head, dv_tok, dv_head}. */
-size_t siq_attn_bwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d);
+size_t siq_attn_bwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
+                                    int deterministic);
 
 int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
                         const void* dout, void* dq, void* dk, void* dv, const int32_t* cu_seqlens_q,
                         const int32_t* cu_seqlens_k, int batch, int max_seqlen_q, int max_seqlen_k,
                         int64_t total_q, int64_t total_k, int hq, int hkv, int d, const int64_t* strides,
-                        float softmax_scale, int causal, void* workspace, size_t workspace_bytes, void* stream);
+                        float softmax_scale, int causal, int deterministic, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /* Allocation-free siq_attn_varlen_fwd.  No counterpart in the reference: it
  * exists for callers that cannot allocate device memory (code under HIP graph
@@ -143,13 +150,15 @@ int siq_attn_varlen_fwd_plan(const void* q, const void* k, const void* v, void* 
                              float softmax_scale, int causal, const void* plan, size_t plan_bytes, void* stream);
 
 /* siq_attn_varlen_bwd over a built plan; the workspace holds the backward's
- * own scratch only (siq_attn_bwd_plan_workspace_bytes). */
-size_t siq_attn_bwd_plan_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d);
+ * own scratch only (siq_attn_bwd_plan_workspace_bytes, for the same
+ * deterministic flag). */
+size_t siq_attn_bwd_plan_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
+                                         int deterministic);
 
 int siq_attn_varlen_bwd_plan(const void* q, const void* k, const void* v, const void* o, const float* lse,
                              const void* dout, void* dq, void* dk, void* dv, int batch, int64_t total_q,
                              int64_t total_k, int hq, int hkv, int d, const int64_t* strides, float softmax_scale,
-                             int causal, const void* plan, size_t plan_bytes, void* workspace,
+                             int causal, int deterministic, const void* plan, size_t plan_bytes, void* workspace,
                              size_t workspace_bytes, void* stream);
 
 /* Varlen attention with the decoder's rotary embedding of q fused in.
@@ -163,7 +172,10 @@ int siq_attn_varlen_bwd_plan(const void* q, const void* k, const void* v, const 
  * siq_attn_rope_bwd_plan takes that q_embed and writes dq with respect to the
  * q BEFORE rotation (bitwise siq_rope_bwd applied to siq_attn_varlen_bwd_plan's
  * dq); dk, dv are those of siq_attn_varlen_bwd_plan (dk with respect to the
- * rotated k).  cos / sin: [total_q, d] bf16 rows, one per packed token.
+ * rotated k).  The backward is the deterministic one (its workspace:
+ * siq_attn_bwd_plan_workspace_bytes(..., 1)): the rotation's backward runs in
+ * the epilogue of its dQ kernel.  cos / sin: [total_q, d] bf16 rows, one per
+ * packed token.
  * strides: fwd[12] = the 8 of siq_attn_varlen_fwd, q_embed (tok, head),
  * cos_tok, sin_tok; bwd[18] = the 16 of siq_attn_varlen_bwd (q = q_embed),
  * cos_tok, sin_tok. */

@@ -33,7 +33,7 @@ _PROTOS = {
     "siq_abi_version": (_i32, []),
     "siq_last_error": (ctypes.c_char_p, []),
     "siq_attn_fwd_workspace_bytes": (_size, [_i32, _i64, _i64, _i32, _i32, _i32]),
-    "siq_attn_bwd_workspace_bytes": (_size, [_i32, _i64, _i64, _i32, _i32, _i32]),
+    "siq_attn_bwd_workspace_bytes": (_size, [_i32, _i64, _i64, _i32, _i32, _i32, _i32]),
     "siq_attn_varlen_fwd": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i64, _i64,
@@ -43,7 +43,7 @@ _PROTOS = {
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
          _c_void_p, _c_void_p, _i32, _i32, _i32, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_i64), _f32, _i32,
-         _c_void_p, _size, _c_void_p],
+         _i32, _c_void_p, _size, _c_void_p],
     ),
     "siq_attn_varlen_fwd_noalloc": (
         _i32,
@@ -51,7 +51,7 @@ _PROTOS = {
          _i32, _i32, _i32, ctypes.POINTER(_i64), _f32, _i32, _c_void_p],
     ),
     "siq_attn_plan_bytes": (_size, [_i32, _i64, _i64]),
-    "siq_attn_bwd_plan_workspace_bytes": (_size, [_i32, _i64, _i64, _i32, _i32, _i32]),
+    "siq_attn_bwd_plan_workspace_bytes": (_size, [_i32, _i64, _i64, _i32, _i32, _i32, _i32]),
     "siq_attn_build_plan": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _i64, _i32, _i32, _i32, _c_void_p, _size,
                                    _c_void_p]),
     "siq_attn_varlen_fwd_plan": (
@@ -62,8 +62,8 @@ _PROTOS = {
     "siq_attn_varlen_bwd_plan": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-         _i32, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_i64), _f32, _i32, _c_void_p, _size, _c_void_p, _size,
-         _c_void_p],
+         _i32, _i64, _i64, _i32, _i32, _i32, ctypes.POINTER(_i64), _f32, _i32, _i32, _c_void_p, _size, _c_void_p,
+         _size, _c_void_p],
     ),
     "siq_attn_rope_fwd_plan": (
         _i32,

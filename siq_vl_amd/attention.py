@@ -232,11 +232,20 @@ def varlen_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlen
     return out, lse
 
 
+# Backward used when a call does not choose (``deterministic=None``): True is
+# the bitwise-reproducible backward (dQ in a kernel of its own), False the one
+# that forms dQ in the dK/dV kernel and sums it with fp32 atomics.
+DETERMINISTIC_DEFAULT = True
+
+
 def varlen_attn_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
                     lse: torch.Tensor, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
-                    max_seqlen_k: int, softmax_scale: float, causal: bool,
-                    plan: AttnPlan | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Returns ``(dq, dk, dv)``, bitwise deterministic."""
+                    max_seqlen_k: int, softmax_scale: float, causal: bool, plan: AttnPlan | None = None,
+                    deterministic: bool | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Returns ``(dq, dk, dv)``: bitwise reproducible when ``deterministic``
+    (None: ``DETERMINISTIC_DEFAULT``), else dQ summed with fp32 atomics (its
+    bits may vary from run to run; dk and dv never do)."""
+    det = DETERMINISTIC_DEFAULT if deterministic is None else bool(deterministic)
     hq, hkv, d = _check_common(q, k, v)
     total_q, total_k = q.shape[0], k.shape[0]
     _check_token_major("out", out, heads=hq, dim=d)
@@ -250,14 +259,14 @@ def varlen_attn_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: tor
     dk = torch.empty((total_k, hkv, d), dtype=q.dtype, device=q.device)
     dv = torch.empty((total_k, hkv, d), dtype=q.dtype, device=q.device)
     L = _lib.lib()
-    ws_bytes = L.siq_attn_bwd_plan_workspace_bytes(pl.batch, total_q, total_k, hq, hkv, d)
+    ws_bytes = L.siq_attn_bwd_plan_workspace_bytes(pl.batch, total_q, total_k, hq, hkv, d, int(det))
     ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=q.device)
     strides = _lib.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
                                 out.stride(0), out.stride(1), dout.stride(0), dout.stride(1), dq.stride(0),
                                 dq.stride(1), dk.stride(0), dk.stride(1), dv.stride(0), dv.stride(1)])
     rc = L.siq_attn_varlen_bwd_plan(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
                                     dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), pl.batch, total_q,
-                                    total_k, hq, hkv, d, strides, float(softmax_scale), int(bool(causal)),
+                                    total_k, hq, hkv, d, strides, float(softmax_scale), int(bool(causal)), int(det),
                                     pl.buf.data_ptr(), pl.buf.numel(), ws.data_ptr(), ws.numel(), _stream(q.device))
     _lib.check(rc, "siq_attn_varlen_bwd_plan")
     return dq, dk, dv
@@ -265,25 +274,25 @@ def varlen_attn_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: tor
 
 class _VarlenAttnFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, scale, causal):
+    def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, deterministic=None):
         q, k, v = (_ensure_token_major(t) for t in (q, k, v))
         hq, hkv = q.shape[1], k.shape[1]
         plan = cached_attn_plan(cu_q, cu_k, q.shape[0], k.shape[0], hq, hkv, causal, q.device)
         out, lse = varlen_attn_fwd(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, plan=plan)
         ctx.save_for_backward(q, k, v, out, lse)
         ctx.plan = plan
-        ctx.args = (max_q, max_k, scale, causal)
+        ctx.args = (max_q, max_k, scale, causal, deterministic)
         return out
 
     @staticmethod
     def backward(ctx, dout):
         q, k, v, out, lse = ctx.saved_tensors
-        max_q, max_k, scale, causal = ctx.args
+        max_q, max_k, scale, causal, deterministic = ctx.args
         plan = ctx.plan
         dout = _ensure_token_major(dout)
         dq, dk, dv = varlen_attn_bwd(dout, q, k, v, out, lse, plan.cu_q, plan.cu_k, max_q, max_k, scale, causal,
-                                     plan=plan)
-        return dq, dk, dv, None, None, None, None, None, None
+                                     plan=plan, deterministic=deterministic)
+        return dq, dk, dv, None, None, None, None, None, None, None
 
 
 def _check_rope_rows(cos: torch.Tensor, sin: torch.Tensor, total_q: int, d: int) -> None:
@@ -345,7 +354,7 @@ def varlen_attn_rope_bwd(dout: torch.Tensor, q_embed: torch.Tensor, k: torch.Ten
     dk = torch.empty((total_k, hkv, d), dtype=q_embed.dtype, device=q_embed.device)
     dv = torch.empty((total_k, hkv, d), dtype=q_embed.dtype, device=q_embed.device)
     L = _lib.lib()
-    ws_bytes = L.siq_attn_bwd_plan_workspace_bytes(pl.batch, total_q, total_k, hq, hkv, d)
+    ws_bytes = L.siq_attn_bwd_plan_workspace_bytes(pl.batch, total_q, total_k, hq, hkv, d, 1)
     ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=q_embed.device)
     q = q_embed
     strides = _lib.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
@@ -426,11 +435,12 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu
                            cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int, dropout_p: float = 0.0,
                            softmax_scale: float | None = None, causal: bool = False,
                            window_size: tuple[int, int] = (-1, -1), softcap: float = 0.0,
-                           alibi_slopes: torch.Tensor | None = None, deterministic: bool = True,
+                           alibi_slopes: torch.Tensor | None = None, deterministic: bool | None = None,
                            return_attn_probs: bool = False, **kwargs: Any) -> torch.Tensor:
     """Varlen attention with the flash-attention varlen call convention.
 
     ``q [total_q, hq, d]``, ``k/v [total_k, hkv, d]`` (bf16); returns ``[total_q, hq, d]``.
+    ``deterministic`` picks the backward (None: ``DETERMINISTIC_DEFAULT``).
     Features outside the reference path (dropout, sliding window, softcap,
     ALiBi, returning probabilities) are rejected, not approximated.
     """
@@ -447,7 +457,7 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu
     if softmax_scale is None:
         softmax_scale = q.shape[-1] ** -0.5
     return _VarlenAttnFn.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), int(max_seqlen_k),
-                               float(softmax_scale), bool(causal))
+                               float(softmax_scale), bool(causal), None if deterministic is None else bool(deterministic))
 
 
 # --------------------------------------------------------------------------- transformers plug-in

@@ -89,6 +89,7 @@ struct AttnParams {
   bf16* dv;
   float* delta;      // [hq, lse_head] rowsum(dO * O) (backward workspace)
   float* lse2;       // [hq, lse_head] LSE * log2(e) (backward workspace)
+  float* dq_acc;     // [total_q, hq, D] fp32 dQ sums of the atomic backward; nullptr: deterministic
   const SeqInfo* seq;
   const QTile* qtiles;       // q tiles ordered by decreasing work; b < 0 = idle
   const KvItem* kvitems;     // dK/dV work items (longest sequences first); b < 0 = idle

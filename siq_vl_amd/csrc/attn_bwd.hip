@@ -1,4 +1,5 @@
-// Varlen flash attention backward for gfx950 (deterministic: no atomics).
+// Varlen flash attention backward for gfx950, deterministic (no atomics) or
+// with atomic dQ.
 //
 // Math (the gradient of the reference's eager attention,
 // transformers models/qwen2/modeling_qwen2.py:150-172): with P = softmax(S),
@@ -39,7 +40,24 @@ namespace siq {
 
 namespace {
 
-template <int D, bool CAUSAL>
+// Atomic dQ (DQ = true, the non-deterministic backward): the dK/dV kernel
+// also forms dQ = dS K, so no second kernel recomputes S and dP.  Each wave
+// writes its 32 x 32 block of dS (bf16) to an LDS exchange buffer [64 q][128
+// kv] (rows padded to 136 elements: consecutive rows start one 16-byte bank
+// group apart, so the row reads below are conflict free and every write of a
+// lane is its base plus a constant); after a barrier wave (g, kq) multiplies
+// the q rows of group g by K for d-tile kq % NDT over the kv quarters of part
+// kq / NDT (all four at D = 128, two at D = 64) and adds the fp32 result to a
+// dQ workspace with vector atomics, issued after the step's closing barrier so
+// that its load wait does not also wait for them.  kv offset o of each 16-kv
+// group is stored at slot o with bits 2 and 3 swapped, so that a row read
+// returns the kv order of a transposed K read (TrRead's krow).
+constexpr int kDsxLd = kBwdBN + 8;
+__device__ __forceinline__ int dsx_slot(int kv) {
+  return (kv & ~15) | (kv & 3) | ((kv & 4) << 1) | ((kv & 8) >> 1);
+}
+
+template <int D, bool CAUSAL, bool DQ>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams p) {
   constexpr int BN = kBwdBN, BM = kBwdBM, NT = 512, NW = NT / 64, NS = 2;
   static_assert(BN == 128 && BM == 64, "128 kv rows (4 x 32) by 64 q rows (2 x 32) per step");
@@ -52,6 +70,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
   static_assert(2 * 4 * NDT * 16 * 64 * 4 <= SMEM * 2, "one reduction round fits the LDS");
   __shared__ __align__(16) bf16 smem[SMEM];
   __shared__ __align__(16) float rowv[NS][2][BM];  // [stage][lse2 | delta][q] (raw, as loaded)
+  __shared__ __align__(16) bf16 dsx[DQ ? BM * kDsxLd : 8];  // dS exchange (atomic dQ)
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int wu = wave_uniform(tid >> 6);
@@ -148,6 +167,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
   constexpr int KPI = (D / 16) / StTile::PERW;  // S / dP k-steps per spread load instruction
   static_assert(KPI >= 1 && (D / 16) % StTile::PERW == 0, "loads spread evenly over the k-steps");
 
+  // atomic dQ: this wave's d-tile and kv quarters
+  constexpr int WPT = 4 / NDT;                  // waves per d-tile
+  const int qdt = kq % NDT, qpart = kq / NDT;   // d-tile, kv-quarter part
+
   if (ns > 0) issue(s0, 0);
   wait_vmem();
   __syncthreads();
@@ -179,7 +202,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
 
     const int wq0 = q0 + 32 * g;  // first q row of this wave
     // kv quarters past the sequence end have nothing to accumulate
-    const bool active = 32 * g < qvalid && kb < si.k_len && (!CAUSAL || wq0 + 31 + off >= kb);
+    auto quarter_active = [&](int qq) {
+      const int kq0 = k0 + 32 * qq;
+      return 32 * g < qvalid && kq0 < si.k_len && (!CAUSAL || wq0 + 31 + off >= kq0);
+    };
+    const bool active = quarter_active(kq);
     if (!active && pf) {
 #pragma unroll
       for (int k = 0; k < StTile::PERW; ++k) issue_k(nl, k);
@@ -250,6 +277,14 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
       pb[1] = pack8(s, 8);
       db[0] = pack8(dp, 0);
       db[1] = pack8(dp, 8);
+      if constexpr (DQ) {
+        // this wave's dS block into the exchange buffer: q = 32 g + 4 h + 8 (r / 4) + r % 4, kv = 32 kq + l32.
+        // kv rows past the sequence end hold the last row's K (their dK / dV rows are never written, but
+        // dQ sums over kv): their dS is written as zero
+        bf16* w = dsx + (32 * g + 4 * h) * kDsxLd + dsx_slot(32 * kq + l32);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) w[(8 * (r >> 2) + (r & 3)) * kDsxLd] = kvvalid ? db[r >> 3][r & 7] : (bf16)0.f;
+      }
       bf16x8 tg[2], tq[2];
       tg[0] = tr.read(Gs, 32 * g, 0);
       tq[0] = tr.read(Qs, 32 * g, 0);
@@ -265,7 +300,43 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
         dk[dt] = mfma32(tq[cur], db[j], dk[dt]);
       }
     }
-    wait_vmem();
+    if constexpr (DQ) {
+      // every wave's dS block is in the exchange buffer after this barrier
+      __syncthreads();
+      // dQ[q][d] = sum dS[q][kv] K[kv][d] for q rows 32 g .., d-tile qdt, this part's kv quarters
+      f32x16 dqa = zero16();
+      bool any = false;
+#pragma unroll
+      for (int u = 0; u < 4 / WPT; ++u) {
+        const int qq = qpart * (4 / WPT) + u;
+        if (!quarter_active(qq)) continue;
+        any = true;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const bf16x8 a = ld_bf16x8(dsx + (32 * g + l32) * kDsxLd + 8 * h + 16 * (2 * qq + kk));
+          const bf16x8 b = tr.read(Ks, 32 * qq + 16 * kk, qdt);
+          dqa = mfma32(a, b, dqa);
+        }
+      }
+      // the next stage's loads first (the atomics below also count in vmcnt), then the sums
+      wait_vmem();
+      if (any) {
+        // wave-uniform base (first row of the group, its q-head) plus a 32-bit lane offset
+        float* base = p.dq_acc + ((int64_t)(si.q_start + wq0) * p.hq + hk * p.n_rep + step % p.n_rep) * D;
+        uint32_t rs = (uint32_t)(p.hq * D);
+        uint32_t lo = (uint32_t)(32 * qdt + perm32(l32)) + (uint32_t)(4 * h) * rs;
+        // recomputed here each step: hoisted out of the loop, the 16 row offsets would hold 16 registers
+        asm volatile("" : "+s"(rs), "+v"(lo));
+        const int rows = qvalid - 32 * g;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = 8 * (r >> 2) + (r & 3);
+          if (i + 4 * h < rows) __builtin_amdgcn_global_atomic_fadd_f32(base + lo + (uint32_t)i * rs, dqa[r]);
+        }
+      }
+    } else {
+      wait_vmem();
+    }
     __syncthreads();
   }
 
@@ -582,16 +653,84 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
   }
 }
 
+// Atomic backward, before the dK/dV kernel: Delta = rowsum(dO o O) and LSE *
+// log2(e) of every (row, q-head), which the dQ kernel publishes in the
+// deterministic backward, and the fp32 dQ sums cleared.  Two lanes per (row,
+// head), lane h summing d = 16 ks + 8 h + i in the dQ kernel's order, so that
+// Delta -- and with it dK and dV -- is bitwise that of the deterministic
+// backward.
+template <int D>
+__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const AttnParams p) {
+  const int h = threadIdx.x & 1;
+  const int64_t npairs = p.total_q * p.hq;
+  for (int64_t pi = (int64_t)blockIdx.x * 128 + (threadIdx.x >> 1); pi < npairs; pi += (int64_t)gridDim.x * 128) {
+    const int64_t row = pi / p.hq;
+    const int hq = (int)(pi - row * p.hq);
+    const bf16* op = p.o + row * p.o_tok + (int64_t)hq * p.o_head + 8 * h;
+    const bf16* gp = p.dout + row * p.do_tok + (int64_t)hq * p.do_head + 8 * h;
+    float* z = p.dq_acc + pi * D + 8 * h;
+    float acc = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      const bf16x8 o = ld_bf16x8(op + 16 * ks), g = ld_bf16x8(gp + 16 * ks);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = __builtin_fmaf((float)g[i], (float)o[i], acc);
+      *reinterpret_cast<f32x4*>(z + 16 * ks) = f32x4{0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<f32x4*>(z + 16 * ks + 4) = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    acc += __shfl_xor(acc, 1);
+    if (h == 0) {
+      const int64_t idx = (int64_t)hq * p.lse_head + row;
+      p.delta[idx] = acc;
+      p.lse2[idx] = p.lse[idx] * kLog2e;
+    }
+  }
+}
+
+// Atomic backward, last: dq = bf16(scale * dQ sums).
+template <int D>
+__global__ __launch_bounds__(256) void attn_bwd_dq_convert_kernel(const AttnParams p) {
+  constexpr int LP = D / 8, PPB = 256 / LP;
+  const int sub = threadIdx.x % LP;
+  const int64_t npairs = p.total_q * p.hq;
+  for (int64_t pi = (int64_t)blockIdx.x * PPB + threadIdx.x / LP; pi < npairs; pi += (int64_t)gridDim.x * PPB) {
+    const int64_t row = pi / p.hq;
+    const int hq = (int)(pi - row * p.hq);
+    const float* a = p.dq_acc + pi * D + 8 * sub;
+    const f32x4 x0 = *reinterpret_cast<const f32x4*>(a), x1 = *reinterpret_cast<const f32x4*>(a + 4);
+    bf16x8 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[i] = (bf16)(x0[i] * p.scale);
+      o[i + 4] = (bf16)(x1[i] * p.scale);
+    }
+    st_bf16x8(p.dq + row * p.dq_tok + (int64_t)hq * p.dq_head + 8 * sub, o);
+  }
+}
+
 template <int D, bool CAUSAL>
 hipError_t launch_bwd_t(const AttnParams& p, int qcap, int kvcap, hipStream_t stream) {
+  const dim3 kvgrid((unsigned)((int64_t)kvcap * p.hkv));
+  if (p.dq_acc != nullptr) {
+    // atomic: Delta / LSE2 and cleared sums, dK/dV with dQ, partial sums, dq
+    const int64_t pairs = p.total_q * p.hq;
+    const int64_t pblocks = std::min<int64_t>((pairs + 127) / 128, 8192);
+    const int64_t blocks = std::min<int64_t>((pairs + 256 / (D / 8) - 1) / (256 / (D / 8)), 8192);
+    if (pblocks > 0) hipLaunchKernelGGL((attn_bwd_prep_kernel<D>), dim3((unsigned)pblocks), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL, true>), kvgrid, dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D>), dim3(min(kMaxSplitTiles * DkvSum<D>::NCH, 512), p.hkv), dim3(256),
+                       0, stream, p);
+    if (blocks > 0)
+      hipLaunchKernelGGL((attn_bwd_dq_convert_kernel<D>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    return hipGetLastError();
+  }
   // dQ first: it also writes Delta and LSE2, which the dK/dV kernel reads
   const dim3 qgrid((unsigned)((int64_t)qcap * p.hq));
   if (p.rcos != nullptr)
     hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL, true>), qgrid, dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL, false>), qgrid, dim3(256), 0, stream, p);
-  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL>), dim3((unsigned)((int64_t)kvcap * p.hkv)), dim3(512), 0, stream,
-                     p);
+  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL, false>), kvgrid, dim3(512), 0, stream, p);
   hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D>), dim3(min(kMaxSplitTiles * DkvSum<D>::NCH, 512), p.hkv), dim3(256), 0, stream,
                      p);
   return hipGetLastError();

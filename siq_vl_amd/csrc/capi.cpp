@@ -66,12 +66,13 @@ PlanLayout plan_layout(int batch, int64_t total_q, int64_t total_k, bool kv) {
 }
 
 // The backward's own scratch beyond the plan: split-tile partial sums,
-// Delta = rowsum(dO o O) and LSE * log2(e).
+// Delta = rowsum(dO o O), LSE * log2(e) and, for the atomic backward, the
+// fp32 dQ sums [total_q][hq][d].
 struct BwdLayout {
-  size_t part, delta, lse2, total;
+  size_t part, delta, lse2, dq_acc, total;
 };
 
-BwdLayout bwd_layout(int64_t total_q, int hq, int d) {
+BwdLayout bwd_layout(int64_t total_q, int hq, int d, bool deterministic) {
   BwdLayout L{};
   size_t off = 0;
   L.part = off;
@@ -80,6 +81,8 @@ BwdLayout bwd_layout(int64_t total_q, int hq, int d) {
   off += align256(sizeof(float) * (size_t)hq * (size_t)total_q);
   L.lse2 = off;
   off += align256(sizeof(float) * (size_t)hq * (size_t)total_q);
+  L.dq_acc = off;
+  if (!deterministic) off += align256(sizeof(float) * (size_t)total_q * (size_t)hq * (size_t)d);
   L.total = off;
   return L;
 }
@@ -144,10 +147,11 @@ size_t siq_attn_fwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k,
   return plan_layout(batch, total_q, total_k, false).total;
 }
 
-size_t siq_attn_bwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d) {
+size_t siq_attn_bwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
+                                    int deterministic) {
   (void)hkv;
   if (batch < 0 || total_q < 0 || total_k < 0 || hq <= 0 || d <= 0) return 0;
-  return plan_layout(batch, total_q, total_k, true).total + bwd_layout(total_q, hq, d).total;
+  return plan_layout(batch, total_q, total_k, true).total + bwd_layout(total_q, hq, d, deterministic != 0).total;
 }
 
 size_t siq_attn_plan_bytes(int batch, int64_t total_q, int64_t total_k) {
@@ -155,12 +159,13 @@ size_t siq_attn_plan_bytes(int batch, int64_t total_q, int64_t total_k) {
   return plan_layout(batch, total_q, total_k, true).total;
 }
 
-size_t siq_attn_bwd_plan_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d) {
+size_t siq_attn_bwd_plan_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
+                                         int deterministic) {
   (void)batch;
   (void)total_k;
   (void)hkv;
   if (total_q < 0 || hq <= 0 || d <= 0) return 0;
-  return bwd_layout(total_q, hq, d).total;
+  return bwd_layout(total_q, hq, d, deterministic != 0).total;
 }
 
 int siq_attn_build_plan(const int32_t* cu_q, const int32_t* cu_k, int batch, int64_t total_q, int64_t total_k,
@@ -265,9 +270,9 @@ int run_fwd(const void* q, const void* k, const void* v, void* o, float* lse, in
 // Backward over a built plan and the backward's own scratch at ws.
 int run_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout, void* dq,
             void* dk, void* dv, int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
-            const int64_t* strides, float scale, int causal, char* plan_base, const PlanLayout& L, char* ws,
-            hipStream_t s, const RopeIn* rope = nullptr) {
-  const BwdLayout B = bwd_layout(total_q, hq, d);
+            const int64_t* strides, float scale, int causal, bool deterministic, char* plan_base,
+            const PlanLayout& L, char* ws, hipStream_t s, const RopeIn* rope = nullptr) {
+  const BwdLayout B = bwd_layout(total_q, hq, d, deterministic);
   siq::AttnParams p{};
   if (rope != nullptr) {
     p.rcos = static_cast<const siq::bf16*>(rope->cos);
@@ -287,6 +292,7 @@ int run_bwd(const void* q, const void* k, const void* v, const void* o, const fl
   p.delta = reinterpret_cast<float*>(ws + B.delta);
   p.lse2 = reinterpret_cast<float*>(ws + B.lse2);
   p.dkv_part = reinterpret_cast<float*>(ws + B.part);
+  p.dq_acc = deterministic ? nullptr : reinterpret_cast<float*>(ws + B.dq_acc);
   set_plan(p, plan_base, L);
   set_common(p, batch, total_q, total_k, hq, hkv, strides, 16, scale);
   const hipError_t e = siq::launch_attn_bwd(p, d, causal != 0, L.qcap, L.kvcap, s);
@@ -335,14 +341,14 @@ int siq_attn_varlen_fwd_plan(const void* q, const void* k, const void* v, void* 
 int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
                         const void* dout, void* dq, void* dk, void* dv, const int32_t* cu_q, const int32_t* cu_k,
                         int batch, int max_q, int max_k, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
-                        const int64_t* strides, float scale, int causal, void* ws, size_t ws_bytes,
-                        void* stream) {
+                        const int64_t* strides, float scale, int causal, int deterministic, void* ws,
+                        size_t ws_bytes, void* stream) {
   int rc = check_attn_common(batch, max_q, max_k, total_q, total_k, hq, hkv, d, scale);
   if (rc || (rc = check_cu(batch, cu_q, cu_k))) return rc;
   if ((rc = check_bwd_tensors(q, k, v, o, lse, dout, dq, dk, dv, total_q, total_k, strides))) return rc;
   if (batch == 0 || (total_q == 0 && total_k == 0)) return ok();
   const PlanLayout L = plan_layout(batch, total_q, total_k, true);
-  const size_t need = L.total + bwd_layout(total_q, hq, d).total;
+  const size_t need = L.total + bwd_layout(total_q, hq, d, deterministic != 0).total;
   if (ws == nullptr || ws_bytes < need || !aligned16(ws))
     return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -350,13 +356,14 @@ int siq_attn_varlen_bwd(const void* q, const void* k, const void* v, const void*
   const hipError_t e = build_plan(base, L, cu_q, cu_k, batch, total_q, total_k, hq, hkv, causal != 0, true, s);
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "schedule launch failed: %s", hipGetErrorString(e));
   return run_bwd(q, k, v, o, lse, dout, dq, dk, dv, batch, total_q, total_k, hq, hkv, d, strides, scale, causal,
-                 base, L, base + L.total, s);
+                 deterministic != 0, base, L, base + L.total, s);
 }
 
 int siq_attn_varlen_bwd_plan(const void* q, const void* k, const void* v, const void* o, const float* lse,
                              const void* dout, void* dq, void* dk, void* dv, int batch, int64_t total_q,
                              int64_t total_k, int hq, int hkv, int d, const int64_t* strides, float scale, int causal,
-                             const void* plan, size_t plan_bytes, void* ws, size_t ws_bytes, void* stream) {
+                             int deterministic, const void* plan, size_t plan_bytes, void* ws, size_t ws_bytes,
+                             void* stream) {
   int rc = check_attn_common(batch, 0, 0, total_q, total_k, hq, hkv, d, scale);
   if (rc) return rc;
   if ((rc = check_bwd_tensors(q, k, v, o, lse, dout, dq, dk, dv, total_q, total_k, strides))) return rc;
@@ -364,11 +371,11 @@ int siq_attn_varlen_bwd_plan(const void* q, const void* k, const void* v, const 
   const PlanLayout L = plan_layout(batch, total_q, total_k, true);
   if (plan == nullptr || plan_bytes < L.total || !aligned16(plan))
     return fail(SIQ_ERR_WORKSPACE, "plan needs %zu bytes (16-byte aligned), got %zu", L.total, plan_bytes);
-  const size_t need = bwd_layout(total_q, hq, d).total;
+  const size_t need = bwd_layout(total_q, hq, d, deterministic != 0).total;
   if (ws == nullptr || ws_bytes < need || !aligned16(ws))
     return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
   return run_bwd(q, k, v, o, lse, dout, dq, dk, dv, batch, total_q, total_k, hq, hkv, d, strides, scale, causal,
-                 static_cast<char*>(const_cast<void*>(plan)), L, static_cast<char*>(ws),
+                 deterministic != 0, static_cast<char*>(const_cast<void*>(plan)), L, static_cast<char*>(ws),
                  static_cast<hipStream_t>(stream));
 }
 
@@ -423,12 +430,12 @@ int siq_attn_rope_bwd_plan(const void* q_embed, const void* k, const void* v, co
   const PlanLayout L = plan_layout(batch, total_q, total_k, true);
   if (plan == nullptr || plan_bytes < L.total || !aligned16(plan))
     return fail(SIQ_ERR_WORKSPACE, "plan needs %zu bytes (16-byte aligned), got %zu", L.total, plan_bytes);
-  const size_t need = bwd_layout(total_q, hq, d).total;
+  const size_t need = bwd_layout(total_q, hq, d, true).total;
   if (ws == nullptr || ws_bytes < need || !aligned16(ws))
     return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
   const RopeIn rope{cos, sin, strides[16], strides[17], nullptr, 0, 0};
   return run_bwd(q_embed, k, v, o, lse, dout, dq, dk, dv, batch, total_q, total_k, hq, hkv, d, strides, scale,
-                 causal, static_cast<char*>(const_cast<void*>(plan)), L, static_cast<char*>(ws),
+                 causal, true, static_cast<char*>(const_cast<void*>(plan)), L, static_cast<char*>(ws),
                  static_cast<hipStream_t>(stream), &rope);
 }
 

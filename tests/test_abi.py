@@ -46,10 +46,12 @@ def test_status_codes_match_header():
 def test_workspace_sizes(lib):
     f = lib.siq_attn_fwd_workspace_bytes
     b = lib.siq_attn_bwd_workspace_bytes
-    assert f(-1, 10, 10, 2, 1, 64) == 0 and b(2, 10, 10, 0, 1, 64) == 0
+    assert f(-1, 10, 10, 2, 1, 64) == 0 and b(2, 10, 10, 0, 1, 64, 1) == 0
     small, big = f(4, 1000, 1000, 12, 2, 128), f(64, 100000, 100000, 12, 2, 128)
     assert 0 < small < big
-    assert b(4, 1000, 1000, 12, 2, 128) > f(4, 1000, 1000, 12, 2, 128)  # bwd adds Delta
+    assert b(4, 1000, 1000, 12, 2, 128, 1) > f(4, 1000, 1000, 12, 2, 128)  # bwd adds Delta
+    # the atomic backward adds its fp32 dQ sums, [total_q, hq, d]
+    assert b(4, 1000, 1000, 12, 2, 128, 0) - b(4, 1000, 1000, 12, 2, 128, 1) >= 1000 * 12 * 128 * 4
     assert f(4, 1000, 1000, 12, 2, 128) % 16 == 0
     w = lib.siq_flce_workspace_bytes
     assert w(-1, 64, 64, 8, 1) == 0
@@ -85,9 +87,10 @@ def test_plan_sizes(lib):
     a, b = lib.siq_attn_plan_bytes(32, 16384, 16384), lib.siq_attn_plan_bytes(200, 32768, 32768)
     assert 0 < a < b and a % 256 == 0
     # the backward call's workspace is a plan plus the backward's own scratch
-    full = lib.siq_attn_bwd_workspace_bytes(32, 16384, 16384, 12, 2, 128)
-    own = lib.siq_attn_bwd_plan_workspace_bytes(32, 16384, 16384, 12, 2, 128)
-    assert full == a + own
+    for det in (1, 0):
+        full = lib.siq_attn_bwd_workspace_bytes(32, 16384, 16384, 12, 2, 128, det)
+        own = lib.siq_attn_bwd_plan_workspace_bytes(32, 16384, 16384, 12, 2, 128, det)
+        assert full == a + own
 
 
 def _strides(n=16):
@@ -133,12 +136,18 @@ def test_attention_empty_batch_is_a_no_op(lib):
 
 
 def test_attention_bwd_validation(lib):
+    for det in (1, 0):
+        rc = lib.siq_attn_varlen_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 8, 16,
+                                     16, 4, 2, 64, _strides(16), 0.1, 1, det, FAKE, 8, None)
+        assert rc == _lib.SIQ_ERR_WORKSPACE
+        rc = lib.siq_attn_varlen_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, FAKE, 2, 8, 8, 16,
+                                     16, 4, 2, 64, _strides(16), 0.1, 1, det, None, 0, None)
+        assert rc == _lib.SIQ_ERR_INVALID_ARGUMENT and b"dq" in lib.siq_last_error()
+    # the atomic backward's workspace is checked against its own (larger) size
+    need_det = lib.siq_attn_bwd_workspace_bytes(2, 16, 16, 4, 2, 64, 1)
     rc = lib.siq_attn_varlen_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 8, 16, 16,
-                                 4, 2, 64, _strides(16), 0.1, 1, FAKE, 8, None)
+                                 4, 2, 64, _strides(16), 0.1, 1, 0, FAKE, need_det, None)
     assert rc == _lib.SIQ_ERR_WORKSPACE
-    rc = lib.siq_attn_varlen_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, FAKE, 2, 8, 8, 16, 16,
-                                 4, 2, 64, _strides(16), 0.1, 1, None, 0, None)
-    assert rc == _lib.SIQ_ERR_INVALID_ARGUMENT and b"dq" in lib.siq_last_error()
 
 
 def test_plan_entry_validation(lib):
@@ -154,11 +163,12 @@ def test_plan_entry_validation(lib):
                None) == _lib.SIQ_ERR_UNSUPPORTED
     assert fwd(None, None, None, None, None, 0, 0, 0, 4, 2, 128, _strides(8), 0.1, 1, None, 0, None) == _lib.SIQ_OK
     bwd = lib.siq_attn_varlen_bwd_plan
-    own = lib.siq_attn_bwd_plan_workspace_bytes(2, 16, 16, 4, 2, 128)
-    assert bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, _strides(16), 0.1, 1,
-               FAKE, need, FAKE, own - 16, None) == _lib.SIQ_ERR_WORKSPACE
-    assert bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, _strides(16), 0.1, 1,
-               None, need, FAKE, own, None) == _lib.SIQ_ERR_WORKSPACE
+    for det in (1, 0):
+        own = lib.siq_attn_bwd_plan_workspace_bytes(2, 16, 16, 4, 2, 128, det)
+        assert bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, _strides(16), 0.1, 1,
+                   det, FAKE, need, FAKE, own - 16, None) == _lib.SIQ_ERR_WORKSPACE
+        assert bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, _strides(16), 0.1, 1,
+                   det, None, need, FAKE, own, None) == _lib.SIQ_ERR_WORKSPACE
 
 
 def test_flce_loss_validation(lib):
@@ -299,7 +309,7 @@ def test_rope_attention_entry_validation(lib):
     assert f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, st, 0.1, 1, FAKE, need - 16,
              None) == _lib.SIQ_ERR_WORKSPACE
     b = lib.siq_attn_rope_bwd_plan
-    own = lib.siq_attn_bwd_plan_workspace_bytes(2, 16, 16, 4, 2, 128)
+    own = lib.siq_attn_bwd_plan_workspace_bytes(2, 16, 16, 4, 2, 128, 1)
     assert b(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, 2, 16, 16, 4, 2, 128, _strides(18),
              0.1, 1, FAKE, need, FAKE, own, None) == _lib.SIQ_ERR_INVALID_ARGUMENT
     assert b(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 16, 4, 2, 128, _strides(18),

@@ -53,7 +53,7 @@ def legacy_fwd_bwd(q, k, v, do, cu, causal):
                                      cu.data_ptr(), cu.data_ptr(), batch, 0, 0, total, total, hq, hkv, d, st, scale,
                                      int(causal), ws.data_ptr(), ws.numel(), s), "fwd")
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    wsb = torch.empty(L.siq_attn_bwd_workspace_bytes(batch, total, total, hq, hkv, d), dtype=torch.uint8,
+    wsb = torch.empty(L.siq_attn_bwd_workspace_bytes(batch, total, total, hq, hkv, d, 1), dtype=torch.uint8,
                       device=DEV)
     st16 = _lib.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
                              out.stride(0), out.stride(1), do.stride(0), do.stride(1), dq.stride(0), dq.stride(1),
@@ -61,7 +61,7 @@ def legacy_fwd_bwd(q, k, v, do, cu, causal):
     _lib.check(L.siq_attn_varlen_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
                                      do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), cu.data_ptr(),
                                      cu.data_ptr(), batch, 0, 0, total, total, hq, hkv, d, st16, scale, int(causal),
-                                     wsb.data_ptr(), wsb.numel(), s), "bwd")
+                                     1, wsb.data_ptr(), wsb.numel(), s), "bwd")
     return out, lse, dq, dk, dv
 
 
