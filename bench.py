@@ -194,6 +194,13 @@ def bench_attention(idx: int, steps: int, warmup: int) -> dict:
     if cfg.backward:
         out["bwd_ms"] = r["bwd_ms"]
         out["bwd_tflops"] = flops_bwd / (r["bwd_ms"] * 1e-3) / 1e12
+        # the two backward modes, graph-replayed over a plan built once (the choice of the default)
+        plan_once = A.build_attn_plan(cu, cu, cfg.total, cfg.total, cfg.hq, cfg.hkv, cfg.causal, dev)
+        o1, l1 = A.varlen_attn_fwd(x["q"], x["k"], x["v"], cu, cu, mx, mx, scale, cfg.causal, plan=plan_once)
+        for det in (True, False):
+            out["bwd_graph_ms_" + ("deterministic" if det else "atomic")] = graphed_ms(
+                lambda: A.varlen_attn_bwd(x["dout"], x["q"], x["k"], x["v"], o1, l1, cu, cu, mx, mx, scale,
+                                          cfg.causal, plan=plan_once, deterministic=det), 5, steps, warmup)
     return out
 
 
@@ -210,6 +217,10 @@ def attn_block(a: dict) -> dict:
     if cfg.backward:
         blk["bwd_ms"] = round(a["bwd_ms"], 4)
         blk["bwd_tflops"] = round(a["bwd_tflops"], 2)
+        blk["bwd_modes_us"] = {"timing": "backward call over a prebuilt plan, 5 per HIP graph, replayed",
+                               "deterministic": round(a["bwd_graph_ms_deterministic"] * 1e3, 1),
+                               "atomic_dq": round(a["bwd_graph_ms_atomic"] * 1e3, 1),
+                               "default": "deterministic" if A.DETERMINISTIC_DEFAULT else "atomic_dq"}
         ach = (a["flops_fwd"] + a["flops_bwd"]) / ((a["fwd_ms"] + a["bwd_ms"]) * 1e-3) / 1e12
         blk["roofline"] = {"bound": "mfma", "kernel": "forward + backward calls", "achieved": round(ach, 2),
                            "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4)}
@@ -632,11 +643,17 @@ def main() -> int:
           f"{att['eager_ms_per_step']:.4f}), {att['tflops']:.1f} TFLOP/s (eager per call: plan "
           f"{att['plan_ms'] * 1e3:.1f} us, fwd {att['fwd_ms'] * 1e3:.1f} us, bwd {att['bwd_ms'] * 1e3:.1f} us); "
           f"shader clock after {clock} MHz", file=sys.stderr, flush=True)
+    print(f"[bench] config 2 backward modes (graph-replayed): deterministic "
+          f"{att['bwd_graph_ms_deterministic'] * 1e3:.1f} us, atomic dQ {att['bwd_graph_ms_atomic'] * 1e3:.1f} us",
+          file=sys.stderr, flush=True)
     others = {}
     for idx in (3, 5, 1):
         others[idx] = bench_attention(idx, leg_steps, args.warmup)
         o = others[idx]
-        extra = f", bwd {o['bwd_ms'] * 1e3:.1f} us" if "bwd_ms" in o else ""
+        extra = ""
+        if "bwd_ms" in o:
+            extra = (f", bwd {o['bwd_ms'] * 1e3:.1f} us; graph-replayed backward deterministic "
+                     f"{o['bwd_graph_ms_deterministic'] * 1e3:.1f} us, atomic dQ {o['bwd_graph_ms_atomic'] * 1e3:.1f} us")
         print(f"[bench] config {idx} attention {o['ms_per_step']:.4f} ms/step, {o['tflops']:.1f} TFLOP/s (fwd "
               f"{o['fwd_ms'] * 1e3:.1f} us{extra})", file=sys.stderr, flush=True)
     ce = None
