@@ -611,6 +611,10 @@ def main() -> int:
     ap.add_argument("--skip-projector", action="store_true")
     ap.add_argument("--skip-splice", action="store_true")
     ap.add_argument("--attn-only", action="store_true", help="attention configs only (no CE / widening legs)")
+    ap.add_argument("--leg", choices=["attn1", "attn2", "attn3", "attn5", "ce", "rope", "rope_attn", "proj", "splice"],
+                    default=None,
+                    help="run one leg only and print its timings (a profiling aid: one rocprofv3 counter pass per "
+                         "leg attributes every dispatch to its workload); no contract JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (3 times): the known-size reference that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -633,6 +637,23 @@ def main() -> int:
         return 0
     if args.attn_only:
         args.skip_ce = args.skip_rope = args.skip_projector = args.skip_splice = True
+    if args.leg is not None:
+        steps = max(args.steps, 1)
+        fns = {"attn1": lambda: bench_attention(1, steps, args.warmup),
+               "attn2": lambda: bench_attention(2, steps, args.warmup),
+               "attn3": lambda: bench_attention(3, steps, args.warmup),
+               "attn5": lambda: bench_attention(5, steps, args.warmup),
+               "ce": lambda: bench_ce(steps, args.warmup, args.ce_chunk),
+               "rope": lambda: bench_rope(steps, args.warmup),
+               "rope_attn": lambda: bench_rope_attention(steps, args.warmup),
+               "proj": lambda: bench_projector(steps, args.warmup),
+               "splice": lambda: bench_splice(steps, args.warmup)}
+        res = fns[args.leg]()
+        torch.cuda.synchronize()
+        out = {k: (round(v, 6) if isinstance(v, float) else v) for k, v in res.items()
+               if isinstance(v, (int, float, str))}
+        print(json.dumps({"leg": args.leg, "steps": steps, **out}), flush=True)
+        return 0
 
     # the headline leg first, then the other configurations (all >= MIN_STEPS timed steps)
     steps = max(args.steps, 1)
