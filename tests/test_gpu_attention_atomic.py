@@ -4,9 +4,12 @@ the C ABI): dQ = dS K formed in the dK/dV kernel and summed with fp32 atomics.
 * small and medium cases against the fp64 CPU oracle (same cases and
   tolerance as the deterministic backward: ||x - x_ref||_F / ||x_ref||_F <=
   2e-2 for dQ, dK, dV);
-* dK and dV are bitwise those of the deterministic backward (the same MFMA
-  sequence; only dQ moves), and dQ agrees with the deterministic dQ to fp32
-  summation order (rel <= 1e-2 after the bf16 rounding of both);
+* at D = 128 dK and dV are bitwise those of the deterministic backward (the
+  same kernel and MFMA sequence; only dQ moves); at D = 64 the deterministic
+  backward runs the one-wave-per-SIMD dK/dV kernel, which sums the two q
+  groups in another order, so there they agree to rel <= 1e-2; dQ agrees with
+  the deterministic dQ to fp32 summation order (rel <= 1e-2 after the bf16
+  rounding of both);
 * no leakage across sequences (the atomics address only the step's own rows);
 * full BASELINE sizes (configs 2, 3, 5) against the per-sequence fp32 torch
   reference;
@@ -61,9 +64,14 @@ def test_atomic_backward_vs_oracle(lengths, hq, hkv, d, causal):
         x = got[name] if name == "dq" else got[name].float().numpy()
         r = rel(x, ref)
         assert r <= TOL, (name, r)
-    # dK / dV do not depend on the dQ mode; dQ only by the fp32 summation order
+    # dK / dV do not depend on the dQ mode (bitwise where both modes run the same dK/dV kernel); dQ only by
+    # the fp32 summation order
     det = run(q, k, v, do, cu, causal, True)
-    assert torch.equal(got["dk"], det["dk"]) and torch.equal(got["dv"], det["dv"])
+    if d == 128:
+        assert torch.equal(got["dk"], det["dk"]) and torch.equal(got["dv"], det["dv"])
+    else:
+        for name in ("dk", "dv"):
+            assert rel(got[name].float().numpy(), det[name].float().numpy()) <= 1e-2, name
     assert rel(got["dq"], det["dq"]) <= 1e-2
 
 
