@@ -611,7 +611,8 @@ def main() -> int:
     ap.add_argument("--skip-projector", action="store_true")
     ap.add_argument("--skip-splice", action="store_true")
     ap.add_argument("--attn-only", action="store_true", help="attention configs only (no CE / widening legs)")
-    ap.add_argument("--leg", choices=["attn1", "attn2", "attn3", "attn5", "ce", "rope", "rope_attn", "proj", "splice"],
+    ap.add_argument("--leg", choices=["attn1", "attn2", "attn3", "attn5", "attn6", "ce", "rope", "rope_attn", "proj",
+                                      "splice"],
                     default=None,
                     help="run one leg only and print its timings (a profiling aid: one rocprofv3 counter pass per "
                          "leg attributes every dispatch to its workload); no contract JSON line")
@@ -643,6 +644,7 @@ def main() -> int:
                "attn2": lambda: bench_attention(2, steps, args.warmup),
                "attn3": lambda: bench_attention(3, steps, args.warmup),
                "attn5": lambda: bench_attention(5, steps, args.warmup),
+               "attn6": lambda: bench_attention(6, steps, args.warmup),
                "ce": lambda: bench_ce(steps, args.warmup, args.ce_chunk),
                "rope": lambda: bench_rope(steps, args.warmup),
                "rope_attn": lambda: bench_rope_attention(steps, args.warmup),
@@ -668,7 +670,7 @@ def main() -> int:
           f"{att['bwd_graph_ms_deterministic'] * 1e3:.1f} us, atomic dQ {att['bwd_graph_ms_atomic'] * 1e3:.1f} us",
           file=sys.stderr, flush=True)
     others = {}
-    for idx in (3, 5, 1):
+    for idx in (3, 5, 1, 6):
         others[idx] = bench_attention(idx, leg_steps, args.warmup)
         o = others[idx]
         extra = ""

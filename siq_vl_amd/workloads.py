@@ -121,6 +121,10 @@ def attn_config(idx: int, seed: int = SEED) -> AttnConfig:
         return AttnConfig("siglip2-large-512-bidir-fwdbwd", 16, 16, 64, False, True, tuple(config3_lengths()))
     if idx == 5:
         return AttnConfig("qwen2.5-1.5b-skewed-fwdbwd", 12, 2, 128, True, True, tuple(config5_lengths(seed)))
+    if idx == 6:
+        # not one of the BASELINE configs: four equal 4096-token causal sequences at the config-2 heads, the
+        # long-sequence reference point for the kernels' inner loops
+        return AttnConfig("qwen2.5-1.5b-4x4096-causal-fwdbwd", 12, 2, 128, True, True, (4096,) * 4)
     raise ValueError(f"no attention config {idx}")
 
 
