@@ -16,16 +16,21 @@ it: config 3 (SigLIP bidirectional) and config 5 (skewed packing) fwd+bwd,
 config 1 forward (also timed on the host CPU: the reference path's fp32 SDPA
 with a block-diagonal mask), and config 4, the fused lm_head cross-entropy
 (tokens/s over all rows, and TFLOP/s at 6 * n * hdim * vocab over all rows and
-over the rows whose label counts).
+over the rows whose label counts).  "Config 6" (four 4096-token causal
+sequences at the config-2 heads) is not a BASELINE configuration: it is the
+long-sequence reference point of the attention kernels.  Each attention
+config also reports its backward in both modes (deterministic, atomic dQ),
+and the RoPE, projector and splice legs run after the CE.
 
 Timing: four consecutive attention steps are captured once as a HIP graph and
 replayed (the same kernels and arguments as eager steps, without the host
 launch gaps between them); HIP events on the replay stream bracket every
 replay (step time = replay time / 4), W warm-up replays first, device
-synchronisation on both sides; the median over K >= 20 replays is reported.  Eager per-call medians are reported beside it.  The
-shader clock is probed right after the timed steps (``gpu_clock_mhz``).  The
-CPU baseline times the reference path's own library calls
-(oracle/cpu_path.py) on bounded samples of the same inputs.
+synchronisation on both sides; the median over K >= 20 replays is reported.
+Eager per-call medians are reported beside it.  The shader clock is probed
+right after the timed steps (``gpu_clock_mhz``).  The CPU baseline times the
+reference path's own library calls (oracle/cpu_path.py) on bounded samples of
+the same inputs.  ``--leg NAME`` runs one leg only (a profiling aid).
 """
 
 from __future__ import annotations

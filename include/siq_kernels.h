@@ -93,7 +93,9 @@ int siq_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, fl
  * own that recomputes S and dP).  deterministic == 0: dQ = dS K is formed in
  * the dK/dV kernel and summed with fp32 atomics in the workspace (the sum
  * order varies from run to run; the workspace grows by total_q * hq * d * 4
- * bytes).  flash-attn's flash_attn_varlen_func(deterministic=...) flag.
+ * bytes; on MI355X it measured 2-3x slower than the deterministic backward at
+ * the SiQ-VL shapes).  flash-attn's flash_attn_varlen_func(deterministic=...)
+ * flag.
  * strides[16] = {q_tok, q_head, k_tok, k_head, v_tok, v_head, o_tok, o_head,
  *                do_tok, do_head, dq_tok, dq_head, dk_tok, dk_head, dv_tok, dv_head}. */
 size_t siq_attn_bwd_workspace_bytes(int batch, int64_t total_q, int64_t total_k, int hq, int hkv, int d,
