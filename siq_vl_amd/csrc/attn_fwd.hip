@@ -25,6 +25,13 @@
 // fp32 accumulators and in bf16), and the O rescale is skipped for the whole
 // wave when no row moved -- after the first block it practically never runs.
 //
+// The softmax costs few VALU instructions per score: q is scaled by
+// scale * log2(e) once (in bf16), the S products start from the accumulator
+// value -m (the row's reference), so a score goes straight into v_exp_f32;
+// the row sum is taken over the bf16 P with v_dot2c_f32_bf16 (two per
+// instruction), the cross-half max / sum with v_permlane32_swap, and the
+// next block's K / V load offsets are computed once per workgroup.
+//
 // With the rotary embedding fused (ROPE), q arrives before rotation: each lane
 // rotates its Q fragment in registers with the cos / sin rows of its token
 // (the same bf16 roundings as transformers' apply_rotary_pos_emb, so the
@@ -117,14 +124,34 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
         qf[ks] = o1;
         qf[ks + HK] = o2;
       }
-      // the rotated rows are stored with the output, after the kv loop: stored
-      // here, every block's wait for its K / V loads would also wait for them
+      // the rotated rows, for the backward (their stores only join the first
+      // block's wait for its K / V loads)
+      if (qvalid) {
+        bf16* qe = p.qe + (int64_t)(si.q_start + qrow) * p.qe_tok + (int64_t)hqi * p.qe_head + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks) st_bf16x8(qe + 16 * ks, qf[ks]);
+      }
     }
+    // q scaled by scale * log2(e) once, in bf16: the products then come out
+    // in the exp2 domain and the softmax needs no multiply per score
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qf[ks][i] = (bf16)((float)qf[ks][i] * c);
   }
+  // full-tile K / V load offsets, computed once
+  uint32_t koff[Tile::PERW], voff[Tile::PERW];
+  kt.full_offsets(p.k_tok, wu, koff);
+  vt.full_offsets(p.v_tok, wu, voff);
+
   f32x16 oacc[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) oacc[i] = zero16();
-  float mref = -INFINITY, lsum = 0.f;  // reference max (log2 units), per-half partial row sum
+  // Scores are kept relative to a per-row reference max mref (log2 units;
+  // -inf until the row sees its first key): the S products start from the
+  // accumulator value -msafe (nb), msafe = mref or 0 while mref is -inf.
+  float mref = -INFINITY, msafe = 0.f, lsum = 0.f;  // lsum: this lane's partial row sum
+  f32x16 nb = zero16();
 
   wait_vmem();
   __syncthreads();
@@ -137,8 +164,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
     const bool more = kb + 1 < nblk;
     if (more) {
       bf16* nx = smem + ((kb + 1) & 1) * STAGE;
-      kt.template issue<true>(kbase + (int64_t)(k0 + BN) * p.k_tok, p.k_tok, si.k_len - k0 - BN, nx, wu);
-      vt.template issue<true>(vbase + (int64_t)(k0 + BN) * p.v_tok, p.v_tok, si.k_len - k0 - BN, nx + TE, wu);
+      const bf16* kn = kbase + (int64_t)(k0 + BN) * p.k_tok;
+      const bf16* vn = vbase + (int64_t)(k0 + BN) * p.v_tok;
+      const int rem = si.k_len - k0 - BN;
+      if (rem >= BN) {
+        kt.issue_full(kn, koff, nx, wu);
+        vt.issue_full(vn, voff, nx + TE, wu);
+      } else {
+        kt.template issue<true>(kn, p.k_tok, rem, nx, wu);
+        vt.template issue<true>(vn, p.v_tok, rem, nx + TE, wu);
+      }
     }
     // a wave whose 32 q rows all lie past the sequence end (the tail of the
     // last q-tile) has nothing to compute; it still stages its loads
@@ -146,8 +181,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
     if (active) {
       // independent accumulators innermost, so consecutive MFMAs never wait on each other
       f32x16 s[BN / 32];
-#pragma unroll
-      for (int t = 0; t < BN / 32; ++t) s[t] = zero16();
       // software pipeline: operand reads run two k-steps ahead of the MFMAs
       constexpr int KS = D / 16, NTL = BN / 32;
       bf16x8 ka[KS][NTL];
@@ -156,7 +189,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
 #pragma unroll
         for (int t = 0; t < NTL; ++t) ka[ks][t] = rr.read(Ks, 32 * t, ks);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+      for (int t = 0; t < NTL; ++t) s[t] = mfma32(ka[0][t], qf[0], nb);
+#pragma unroll
+      for (int ks = 1; ks < KS; ++ks)
 #pragma unroll
         for (int t = 0; t < NTL; ++t) s[t] = mfma32(ka[ks][t], qf[ks], s[t]);
       __builtin_amdgcn_sched_group_barrier(0x100, 2 * NTL, 0);
@@ -174,36 +209,43 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) s[t][r] = (32 * t + 8 * (r >> 2) + (r & 3) > rel) ? -INFINITY : s[t][r];
       }
-      float mx = -INFINITY;
+      float mx = -INFINITY;  // block max relative to msafe
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-      mx = wave_max_xor32(mx) * c;
-      const bool grow = mx > mref + kRescaleLog2;
+      mx = half_max(mx);
+      // a row moves its reference when it sees its first key or when the
+      // block max exceeds the reference by more than 2^kRescaleLog2
+      const bool grow = mx > (mref == -INFINITY ? -INFINITY : kRescaleLog2);
       if (__any(grow)) {
         // rows that did not grow keep alpha = 1 (also when their max is still -inf)
-        const float alpha = grow ? exp2f_fast(mref - mx) : 1.f;
-        mref = grow ? mx : mref;
+        const float mnew = grow ? msafe + mx : mref;
+        const float alpha = grow ? exp2f_fast(mref - mnew) : 1.f;
+        const float delta = grow ? mx : 0.f;
+        mref = mnew;
+        msafe = mref == -INFINITY ? 0.f : mref;
         lsum *= alpha;
+        if (kb > 0) {
 #pragma unroll
-        for (int i = 0; i < D / 32; ++i) oacc[i] *= alpha;
+          for (int i = 0; i < D / 32; ++i) oacc[i] *= alpha;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) nb[i] = -msafe;
+#pragma unroll
+        for (int t = 0; t < BN / 32; ++t) s[t] -= delta;
       }
-      const float msafe = mref == -INFINITY ? 0.f : mref;
-      float ps = 0.f;
       bf16x8 pb[BN / 16];
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e = exp2f_fast(__builtin_fmaf(s[t][r], c, -msafe));
-          s[t][r] = e;
-          ps += e;
-        }
+        for (int r = 0; r < 16; ++r) s[t][r] = exp2f_fast(s[t][r]);
         pb[2 * t] = pack8(s[t], 0);
         pb[2 * t + 1] = pack8(s[t], 8);
       }
-      lsum += ps;
+      // the row sum over the bf16 P that the PV products use
+#pragma unroll
+      for (int st = 0; st < BN / 16; ++st) lsum = sum8_bf16(pb[st], lsum);
 #pragma unroll
       for (int st = 0; st < BN / 16; ++st)
 #pragma unroll
@@ -213,7 +255,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
     __syncthreads();
   }
 
-  const float ltot = wave_sum_xor32(lsum);
+  const float ltot = half_sum(lsum);
   if (qvalid) {
     const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
     bf16* op = p.out + (int64_t)(si.q_start + qrow) * p.o_tok + (int64_t)hqi * p.o_head;
@@ -230,11 +272,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
     if (h == 0) {
       p.lse[(int64_t)hqi * p.lse_head + si.q_start + qrow] =
           ltot > 0.f ? (mref + __log2f(ltot)) * kLn2 : -INFINITY;
-    }
-    if constexpr (ROPE) {
-      bf16* qe = p.qe + (int64_t)(si.q_start + qrow) * p.qe_tok + (int64_t)hqi * p.qe_head + 8 * h;
-#pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) st_bf16x8(qe + 16 * ks, qf[ks]);
     }
   }
 }

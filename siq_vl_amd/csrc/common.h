@@ -123,4 +123,29 @@ __device__ __forceinline__ void rope_bwd8(const bf16x8& g1, const bf16x8& g2, co
 __device__ __forceinline__ float wave_max_xor32(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 __device__ __forceinline__ float wave_sum_xor32(float x) { return x + __shfl_xor(x, 32); }
 
+// The same two reductions with gfx950's v_permlane32_swap (a VALU exchange of
+// the wave's halves, no LDS round trip).  Every lane of the wave must be
+// active.  r[0] holds x of lanes 0..31 in both halves, r[1] x of lanes 32..63,
+// so both halves get bitwise the same result.
+__device__ __forceinline__ float half_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __builtin_amdgcn_fmed3f(__uint_as_float(r[0]), __uint_as_float(r[1]), INFINITY);
+}
+__device__ __forceinline__ float half_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum of the 8 bf16 of v plus acc, two per v_dot2c_f32_bf16 (products with 1
+// are exact; fp32 accumulation).
+__device__ __forceinline__ float sum8_bf16(const bf16x8& v, float acc) {
+  const bf16x2 one = {(bf16)1.f, (bf16)1.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bf16x2 pr = {v[2 * i], v[2 * i + 1]};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
+  }
+  return acc;
+}
+
 }  // namespace siq

@@ -77,6 +77,24 @@ struct LdsTile {
     for (int k = 0; k < PERW; ++k) issue_one<UNTRACKED>(k, gbase, stride, nrows, lds, wu);
   }
 
+  // Element offsets (from the tile's first row) of this wave's PERW
+  // instructions for a whole tile (nrows >= ROWS), computed once so that a
+  // loop over whole tiles issues them without address arithmetic.
+  __device__ __forceinline__ void full_offsets(int64_t stride, int wu, uint32_t (&o)[PERW]) const {
+#pragma unroll
+    for (int k = 0; k < PERW; ++k) o[k] = (uint32_t)((wu * PERW + k) * RPI + lrow) * (uint32_t)stride + coff[k % PAT];
+  }
+
+  // A whole tile from the offsets of full_offsets, untracked (as issue<true>).
+  __device__ __forceinline__ void issue_full(const bf16* gbase, const uint32_t (&o)[PERW], bf16* lds, int wu) const {
+#pragma unroll
+    for (int k = 0; k < PERW; ++k) {
+      const uint32_t la = (uint32_t)(uintptr_t)(lds_void*)(lds + (wu * PERW + k) * 512);
+      asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(o[k] << 1), "s"(gbase), "{m0}"(la)
+                   : "memory");
+    }
+  }
+
   // Instruction k (< PERW) of this wave's share, so that a caller can spread
   // its loads between other work.
   template <bool UNTRACKED = false>
