@@ -24,7 +24,9 @@ sequence leaves a sequence bit-identical; permuting sequences permutes the
 output; GQA heads with equal q give equal o; shifting K by a constant leaves O
 unchanged), a library cross-check against torch scaled_dot_product_attention
 with an explicit block-diagonal mask, central finite differences of the
-backward, and the identity that each row of dS sums to zero.
+backward, and the identity that each row of dS sums to zero; the stored-output
+form of the backward's row term matches the exact one when given the exact
+output.
 """
 
 from __future__ import annotations
@@ -99,9 +101,18 @@ def attention_fwd(q, k, v, cu_q, cu_k, scale: float, causal: bool, q_block: int 
     return out, lse
 
 
-def attention_bwd(dout, q, k, v, cu_q, cu_k, scale: float, causal: bool, q_block: int = 512):
-    """Exact fp64 gradients (dq, dk, dv) of attention_fwd's output w.r.t. q, k, v."""
+def attention_bwd(dout, q, k, v, cu_q, cu_k, scale: float, causal: bool, q_block: int = 512, out=None):
+    """Exact fp64 gradients (dq, dk, dv) of attention_fwd's output w.r.t. q, k, v.
+
+    With ``out`` ([Tq, Hq, D], the forward output as stored, e.g. rounded to
+    bf16) the row term rowsum(P o dP) is taken as rowsum(dO o out) instead --
+    FlashAttention-2's D_i = rowsum(dO_i o O_i) (Dao 2023, Algorithm 2), which
+    fused attention backwards compute from the stored output.  The two agree
+    exactly when ``out`` is the exact output; they part where P is close to
+    one-hot and K is large, since the rounding of ``out`` then dominates
+    dP - D."""
     dout, q, k, v = _f64(dout), _f64(q), _f64(k), _f64(v)
+    o_st = None if out is None else _f64(out)
     cq, ck = _cu(cu_q), _cu(cu_k)
     tq, hq, d = q.shape
     hkv = k.shape[1]
@@ -125,7 +136,11 @@ def attention_bwd(dout, q, k, v, cu_q, cu_k, scale: float, causal: bool, q_block
                 p, _ = _probs(qb, kb, scale, vis_all[r0:r1])                 # [rep, n, lk]
                 dv[ks:ke, hk] += np.einsum("rnk,rnd->kd", p, gb)
                 dp = np.einsum("rnd,kd->rnk", gb, vb)
-                delta = (p * dp).sum(axis=-1, keepdims=True)
+                if o_st is None:
+                    delta = (p * dp).sum(axis=-1, keepdims=True)
+                else:
+                    ob = np.transpose(o_st[qs + r0:qs + r1, heads], (1, 0, 2))
+                    delta = (gb * ob).sum(axis=-1, keepdims=True)
                 ds = p * (dp - delta)
                 dq[qs + r0:qs + r1, heads] = np.transpose(scale * (ds @ kb), (1, 0, 2))
                 dk[ks:ke, hk] += scale * np.einsum("rnk,rnd->kd", ds, qb)

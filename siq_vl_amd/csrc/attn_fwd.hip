@@ -25,12 +25,12 @@
 // fp32 accumulators and in bf16), and the O rescale is skipped for the whole
 // wave when no row moved -- after the first block it practically never runs.
 //
-// The softmax costs few VALU instructions per score: q is scaled by
-// scale * log2(e) once (in bf16), the S products start from the accumulator
-// value -m (the row's reference), so a score goes straight into v_exp_f32;
-// the row sum is taken over the bf16 P with v_dot2c_f32_bf16 (two per
-// instruction), the cross-half max / sum with v_permlane32_swap, and the
-// next block's K / V load offsets are computed once per workgroup.
+// The softmax costs few VALU instructions per score: one v_fma_f32 (scale *
+// log2(e) and the row's reference, applied to the fp32 score, so large
+// logits keep fp32 accuracy) feeding v_exp_f32; the row sum is taken over
+// the bf16 P with v_dot2c_f32_bf16 (two per instruction), the cross-half max
+// / sum with v_permlane32_swap, and the next block's K / V load offsets are
+// computed once per workgroup.
 //
 // With the rotary embedding fused (ROPE), q arrives before rotation: each lane
 // rotates its Q fragment in registers with the cos / sin rows of its token
@@ -132,12 +132,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
         for (int ks = 0; ks < D / 16; ++ks) st_bf16x8(qe + 16 * ks, qf[ks]);
       }
     }
-    // q scaled by scale * log2(e) once, in bf16: the products then come out
-    // in the exp2 domain and the softmax needs no multiply per score
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qf[ks][i] = (bf16)((float)qf[ks][i] * c);
   }
   // full-tile K / V load offsets, computed once
   uint32_t koff[Tile::PERW], voff[Tile::PERW];
@@ -147,11 +141,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   f32x16 oacc[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) oacc[i] = zero16();
-  // Scores are kept relative to a per-row reference max mref (log2 units;
-  // -inf until the row sees its first key): the S products start from the
-  // accumulator value -msafe (nb), msafe = mref or 0 while mref is -inf.
+  // Scores are taken relative to a per-row reference max mref (log2 units;
+  // -inf until the row sees its first key); msafe = mref, or 0 while mref is -inf.
   float mref = -INFINITY, msafe = 0.f, lsum = 0.f;  // lsum: this lane's partial row sum
-  f32x16 nb = zero16();
 
   wait_vmem();
   __syncthreads();
@@ -189,7 +181,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
 #pragma unroll
         for (int t = 0; t < NTL; ++t) ka[ks][t] = rr.read(Ks, 32 * t, ks);
 #pragma unroll
-      for (int t = 0; t < NTL; ++t) s[t] = mfma32(ka[0][t], qf[0], nb);
+      for (int t = 0; t < NTL; ++t) s[t] = mfma32(ka[0][t], qf[0], zero16());
 #pragma unroll
       for (int ks = 1; ks < KS; ++ks)
 #pragma unroll
@@ -209,37 +201,31 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) s[t][r] = (32 * t + 8 * (r >> 2) + (r & 3) > rel) ? -INFINITY : s[t][r];
       }
-      float mx = -INFINITY;  // block max relative to msafe
+      float mx = -INFINITY;
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-      mx = half_max(mx);
+      mx = half_max(mx) * c;  // block max, log2 units
       // a row moves its reference when it sees its first key or when the
       // block max exceeds the reference by more than 2^kRescaleLog2
-      const bool grow = mx > (mref == -INFINITY ? -INFINITY : kRescaleLog2);
+      const bool grow = mx > mref + kRescaleLog2;
       if (__any(grow)) {
         // rows that did not grow keep alpha = 1 (also when their max is still -inf)
-        const float mnew = grow ? msafe + mx : mref;
-        const float alpha = grow ? exp2f_fast(mref - mnew) : 1.f;
-        const float delta = grow ? mx : 0.f;
-        mref = mnew;
+        const float alpha = grow ? exp2f_fast(mref - mx) : 1.f;
+        mref = grow ? mx : mref;
         msafe = mref == -INFINITY ? 0.f : mref;
         lsum *= alpha;
         if (kb > 0) {
 #pragma unroll
           for (int i = 0; i < D / 32; ++i) oacc[i] *= alpha;
         }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) nb[i] = -msafe;
-#pragma unroll
-        for (int t = 0; t < BN / 32; ++t) s[t] -= delta;
       }
       bf16x8 pb[BN / 16];
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[t][r] = exp2f_fast(s[t][r]);
+        for (int r = 0; r < 16; ++r) s[t][r] = exp2f_fast(__builtin_fmaf(s[t][r], c, -msafe));
         pb[2 * t] = pack8(s[t], 0);
         pb[2 * t + 1] = pack8(s[t], 8);
       }

@@ -176,3 +176,25 @@ def test_backward_identities():
     g2 = oa.attention_bwd(do, q, k + shift, v, cu, cu, 0.5, True)
     np.testing.assert_allclose(g1[0], g2[0], rtol=1e-9, atol=1e-11)
     np.testing.assert_allclose(g1[2], g2[2], rtol=1e-9, atol=1e-11)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_backward_stored_output_row_term(causal):
+    lengths = [11, 5]
+    cu = cu_of(lengths)
+    t = cu[-1]
+    q, k, v, do = rand((t, 4, 8), 40), rand((t, 2, 8), 41), rand((t, 2, 8), 42), rand((t, 4, 8), 43)
+    o, _ = oa.attention_fwd(q, k, v, cu, cu, 0.4, causal)
+    exact = oa.attention_bwd(do, q, k, v, cu, cu, 0.4, causal)
+    # the exact output gives the exact row term: rowsum(dO o O) = rowsum(P o dP)
+    stored = oa.attention_bwd(do, q, k, v, cu, cu, 0.4, causal, out=o)
+    for a, b in zip(exact, stored):
+        np.testing.assert_allclose(b, a, rtol=1e-10, atol=1e-12)
+    # a changed output shifts D_i by e_i = rowsum(dO_i o (O'_i - O_i)): dV stays,
+    # dQ_i moves by -scale e_i sum_j P_ij K_j (P K is attention with V = K)
+    o2 = o + 0.1 * rand(o.shape, 44)
+    moved = oa.attention_bwd(do, q, k, v, cu, cu, 0.4, causal, out=o2)
+    np.testing.assert_allclose(moved[2], exact[2], rtol=1e-12, atol=1e-12)
+    pk, _ = oa.attention_fwd(q, k, k, cu, cu, 0.4, causal)
+    e = (do * (o2 - o)).sum(-1, keepdims=True)
+    np.testing.assert_allclose(moved[0] - exact[0], -0.4 * e * pk, rtol=1e-9, atol=1e-11)
