@@ -28,9 +28,10 @@
 //     once for both gradient GEMMs.
 //  3. dH GEMM  dH_c^T = W^T dZ_c^T (split over the vocab) and
 //  4. dW GEMM  dW^T = H_c^T dZ_c.
-// With several chunks dW accumulates in an fp32 workspace; whether a chunk
-// starts, continues or finishes that sum is decided on the device from the
-// valid-row count, so chunks past the valid rows cost nothing.  Every
+// With several chunks dW accumulates over them: in dW itself (bf16) when the
+// valid rows span two chunks, in an fp32 workspace when they span more;
+// whether a chunk starts, continues or finishes that sum is decided on the
+// device from the valid-row count, so chunks past the valid rows cost nothing.  Every
 // reduction has a fixed order, so results are bitwise reproducible.
 //
 // Loss only (no gradient wanted, e.g. evaluation under torch.no_grad): the
@@ -364,12 +365,17 @@ __global__ __launch_bounds__(NT) void flce_dw_kernel(const DwArgs p) {
   // The chunk's part in the sum over chunks, from the valid-row count: the
   // first chunk starts it, the one holding the last valid row finishes it
   // (bf16 store), chunks past it do nothing.  A single chunk (or no valid
-  // row at all) stores bf16 directly.  mode 0: bf16 store; 1: fp32 store;
-  // 2: fp32 add; 3: fp32 add + bf16 store.
+  // row at all) stores bf16 directly.  Over two chunks the first one's sum is
+  // kept in dW itself, in bf16, and the second adds to it: dW is rounded
+  // twice, and the fp32 [V, hdim] round trip (twice dW's size, written and
+  // read back) is saved.  Over more chunks the sum stays in fp32.
+  // mode 0: bf16 store; 1: fp32 store; 2: fp32 add; 3: fp32 add + bf16
+  // store; 4: bf16 add.
   const int64_t nvt_all = *p.nvalid;
   if (p.c0 > 0 && p.c0 >= nvt_all) return;
   const bool last = p.c0 + p.chunk >= nvt_all;
-  const int mode = p.c0 == 0 ? (last ? 0 : 1) : (last ? 3 : 2);
+  const bool two = nvt_all <= 2 * p.chunk;
+  const int mode = p.c0 == 0 ? (last || two ? 0 : 1) : (two ? 4 : (last ? 3 : 2));
   // tokens past the last 64-row step with a valid row are skipped (those up to
   // it are zero padding)
   const int64_t nv = nvt_all - p.c0;
@@ -395,9 +401,16 @@ __global__ __launch_bounds__(NT) void flce_dw_kernel(const DwArgs p) {
           hi[i] = acc[a][b][8 * jj + 4 + i];
         }
         float* a32 = p.acc32 + v * p.hdim + hh;
-        if (mode >= 2) {
+        if (mode == 2 || mode == 3) {
           lo += *reinterpret_cast<const f32x4*>(a32);
           hi += *reinterpret_cast<const f32x4*>(a32 + 4);
+        } else if (mode == 4) {
+          const bf16x8 prev = ld_bf16x8(p.dw + v * p.hdim + hh);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            lo[i] += (float)prev[i];
+            hi[i] += (float)prev[4 + i];
+          }
         }
         if (mode == 1 || mode == 2) {
           *reinterpret_cast<f32x4*>(a32) = lo;
@@ -612,7 +625,9 @@ Layout layout(int64_t n, int64_t hdim, int64_t V, int64_t chunk, bool need_dh, b
   L.part = off;
   if (need_dh && L.splits > 1) off += al(sizeof(float) * (size_t)(L.splits * L.chunk * hdim));
   L.acc32 = off;
-  if (need_dw && nchunks > 1) off += al(sizeof(float) * (size_t)(V * hdim));
+  // the fp32 dW sum: only when the valid rows may span more than two chunks
+  // (over two, the first chunk's sum is kept in dW itself)
+  if (need_dw && nchunks > 2) off += al(sizeof(float) * (size_t)(V * hdim));
   const int64_t npad = ((n > 0 ? n : 1) + 255) / 256 * 256;
   L.rows = off;
   off += al(sizeof(int32_t) * (size_t)npad);

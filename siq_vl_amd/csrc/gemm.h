@@ -101,15 +101,21 @@ struct SlabLoad {
       }
       return;
     }
+    // a uniform base at the slab's first row / chunk and 32-bit offsets
+    // clamped to its last valid row / chunk, as in the full case (no per-lane
+    // 64-bit addresses).  A slab that starts outside the operand (a tile wholly
+    // past its M / N extent; k-steps always start inside) is not loaded: its
+    // products only reach outputs that are never stored.
+    const int64_t fr = KC ? r0 : k0, fc = KC ? k0 : r0;
+    if (fr >= op.rows || fc + 8 > op.cols) return;
+    const bf16* base = op.base + fr * op.ld + fc;
+    const int rmax = (int)min(op.rows - 1 - fr, (int64_t)255), cmax = (int)min(op.cols - 8 - fc, (int64_t)248);
 #pragma unroll
     for (int k = 0; k < PERW; ++k) {
       const int r = KC ? wrow + 8 * k + lrow : wrow + 2 * k + lrow;
       const int c = KC ? (lpc ^ swz_kc(r)) : (lpc ^ swz_nkc(r));
-      int64_t gr = KC ? r0 + r : k0 + r;
-      int64_t gc = KC ? k0 + 8 * c : r0 + 8 * c;
-      gr = gr < op.rows ? gr : op.rows - 1;
-      gc = gc < op.cols ? gc : op.cols - 8;
-      dma16(op.base + gr * op.ld + gc, lds + (wu * PERW + k) * 512);
+      const int gr = min(r, rmax), gc = min(8 * c, cmax);
+      dma16(base, (uint32_t)(gr * (int)op.ld + gc), lds + (wu * PERW + k) * 512);
     }
   }
 };
