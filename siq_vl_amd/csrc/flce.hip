@@ -172,43 +172,57 @@ struct RowArgs {
   int rewrite;           // 0: loss only (E was never stored)
 };
 
-// One wave (one workgroup) per token row.  lse2 = M + log2(sum_t s_t
+// One workgroup (four waves) per token row.  lse2 = M + log2(sum_t s_t
 // 2^(m_t - M)); then the row of E becomes dZ = E * f_t - g [v == y], f_t =
 // 2^(m_t - lse2) * g, in fp32 and rounded to bf16 once (zero for an ignored
 // row: g = 0).  The factors f_t are computed once per tile into LDS, in
 // segments of kRowSegTiles tiles, so the streaming loop does one LDS read and
-// eight multiplies per 16 bytes.
-constexpr int kRowSegTiles = 1024;
-__global__ __launch_bounds__(64) void flce_row_kernel(const RowArgs p) {
+// eight multiplies per 16 bytes.  Four waves per row (rather than one) split
+// the per-row reductions over the tile statistics, which precede the
+// streaming, four ways.
+constexpr int kRowSegTiles = 1024, kRowThreads = 256;
+__global__ __launch_bounds__(kRowThreads) void flce_row_kernel(const RowArgs p) {
+  constexpr int RT = kRowThreads, NWR = RT / 64;
   __shared__ float fsh[kRowSegTiles];
-  const int lane = threadIdx.x;
+  __shared__ float red[NWR];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t row = blockIdx.x;
   // rows past the last token tile with a valid row are read by no GEMM
   if (row >= p.nc || row >= ((*p.nvalid - p.c0 + BJ - 1) / BJ) * BJ) return;
   const float* m = p.mpart + row * p.nvt;
   const float* s = p.spart + row * p.nvt;
   float mx = -INFINITY;
-  for (int64_t t = lane; t < p.nvt; t += 64) mx = fmaxf(mx, m[t]);
+  for (int64_t t = tid; t < p.nvt; t += RT) mx = fmaxf(mx, m[t]);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) red[w] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NWR; ++i) mx = fmaxf(mx, red[i]);
+  __syncthreads();  // red is reused below
   float sum = 0.f;
-  for (int64_t t = lane; t < p.nvt; t += 64) sum += s[t] * exp2f_fast(m[t] - mx);
+  for (int64_t t = tid; t < p.nvt; t += RT) sum += s[t] * exp2f_fast(m[t] - mx);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+  if (lane == 0) red[w] = sum;
+  __syncthreads();
+  sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < NWR; ++i) sum += red[i];  // fixed order: every thread gets the same sum
   const float lse2 = mx + __log2f(sum);
   const int64_t yv = p.y[row];
   const bool valid = yv != p.ignore_index && yv >= 0 && yv < p.V;
   const float gv = valid ? *p.invden : 0.f;
-  if (lane == 0) p.loss_row[row] = valid ? lse2 * kLn2 - p.zy[row] : 0.f;
+  if (tid == 0) p.loss_row[row] = valid ? lse2 * kLn2 - p.zy[row] : 0.f;
   if (!p.rewrite) return;
-  // dZ, 8 columns per lane per chunk (V is a multiple of 8, so a chunk never
+  // dZ, 8 columns per thread per chunk (V is a multiple of 8, so a chunk never
   // straddles the row end; 8 aligned columns never straddle a 256-column
   // tile: chunk c lies in tile c / 32).  An ignored row's dZ is zero: written
   // without reading E.
   bf16* e = p.E + row * p.V;
   const int64_t nchunk = p.V / 8;
   if (gv == 0.f) {
-    for (int64_t c = lane; c < nchunk; c += 64) st_bf16x8(e + 8 * c, zero_bf16x8());
+    for (int64_t c = tid; c < nchunk; c += RT) st_bf16x8(e + 8 * c, zero_bf16x8());
     return;
   }
   auto chunk = [&](const bf16x8& x, float fv, int64_t c) {
@@ -223,26 +237,27 @@ __global__ __launch_bounds__(64) void flce_row_kernel(const RowArgs p) {
     }
     st_bf16x8(e + v0, o);
   };
-  // U chunks per lane in flight: lane chunks c + 64 u sit in tiles c / 32 + 2 u
-  // (the pass streams E in and dZ out at the device's mixed read / write rate;
-  // deeper unrolling and non-temporal accesses measured no faster)
+  // U chunks per thread in flight: thread chunks c + RT u sit in tiles
+  // c / 32 + (RT / 32) u (the pass streams E in and dZ out at the device's
+  // mixed read / write rate; deeper unrolling, loading the next chunks before
+  // this U's stores, and non-temporal accesses measured no faster)
   constexpr int U = 8;
   for (int64_t t0 = 0; t0 < p.nvt; t0 += kRowSegTiles) {
     const int nt = (int)min((int64_t)kRowSegTiles, p.nvt - t0);
     __syncthreads();  // the previous segment's factors are no longer read
-    for (int t = lane; t < nt; t += 64) fsh[t] = exp2f_fast(m[t0 + t] - lse2) * gv;
+    for (int t = tid; t < nt; t += RT) fsh[t] = exp2f_fast(m[t0 + t] - lse2) * gv;
     __syncthreads();
     const int64_t cb = 32 * t0, ce = min(nchunk, 32 * (t0 + nt));
-    int64_t c = cb + lane;
-    for (; c + 64 * (U - 1) < ce; c += 64 * U) {
+    int64_t c = cb + tid;
+    for (; c + RT * (U - 1) < ce; c += RT * U) {
       bf16x8 x[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) x[u] = ld_bf16x8(e + 8 * (c + 64 * u));
+      for (int u = 0; u < U; ++u) x[u] = ld_bf16x8(e + 8 * (c + RT * u));
       const int tb = (int)((c - cb) >> 5);
 #pragma unroll
-      for (int u = 0; u < U; ++u) chunk(x[u], fsh[tb + 2 * u], c + 64 * u);
+      for (int u = 0; u < U; ++u) chunk(x[u], fsh[tb + (RT / 32) * u], c + RT * u);
     }
-    for (; c < ce; c += 64) chunk(ld_bf16x8(e + 8 * c), fsh[(c - cb) >> 5], c);
+    for (; c < ce; c += RT) chunk(ld_bf16x8(e + 8 * c), fsh[(c - cb) >> 5], c);
   }
 }
 
@@ -720,7 +735,7 @@ hipError_t flce_run(const FlceArgs& a, hipStream_t stream) {
     rw.V = V;
     rw.ignore_index = a.ignore_index;
     rw.rewrite = grads ? 1 : 0;
-    hipLaunchKernelGGL(flce_row_kernel, dim3((unsigned)nc), dim3(64), 0, stream, rw);
+    hipLaunchKernelGGL(flce_row_kernel, dim3((unsigned)nc), dim3(kRowThreads), 0, stream, rw);
     if (!grads) continue;
 
     DhArgs dh{};
