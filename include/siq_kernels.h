@@ -214,9 +214,10 @@ int siq_attn_rope_bwd_plan(const void* q_embed, const void* k, const void* v, co
  * The logits are produced chunk_tokens rows at a time: only the softmax
  * numerators of one chunk (chunk_tokens x vocab bf16, each relative to the max
  * of its 256-column tile) ever exist, in the workspace; chunks count rows
- * whose label counts (ignored rows are compacted away first).  With more than
- * one chunk dweight is summed over chunks in an fp32 [vocab, hdim] workspace
- * buffer.
+ * whose label counts (ignored rows are compacted away first).  Over two
+ * chunks dweight is summed in dweight itself (the first chunk's sum rounded to
+ * bf16 once); over more it is summed in an fp32 [vocab, hdim] workspace
+ * buffer, which the workspace holds whenever n exceeds two chunks.
  * ------------------------------------------------------------------------- */
 size_t siq_flce_workspace_bytes(int64_t n, int64_t hdim, int64_t vocab, int64_t chunk_tokens, int need_dweight);
 
