@@ -82,6 +82,22 @@ def test_flce_default_workspace_bound_at_config4(lib):
     assert lib.siq_flce_loss_workspace_bytes(n, hdim, vocab) < 128 << 20
 
 
+def test_flce_fp32_dw_sum_only_beyond_two_chunks(lib):
+    """Over at most two chunks dW is summed in dW itself (bf16), so the
+    workspace holds the fp32 [vocab, hdim] sum only when the rows may span a
+    third chunk: one row more than two chunks adds exactly that buffer (plus
+    the per-row pieces of one more row)."""
+    hdim, vocab, chunk = 256, 4096, 512
+    w = lib.siq_flce_workspace_bytes
+    two, three = w(2 * chunk, hdim, vocab, chunk, 1), w(2 * chunk + 1, hdim, vocab, chunk, 1)
+    fp32_sum = vocab * hdim * 4
+    assert fp32_sum <= three - two < fp32_sum + 4096 + 256 * (hdim * 2 + 16)
+    # without dweight there is no sum either way
+    assert w(2 * chunk + 1, hdim, vocab, chunk, 0) - w(2 * chunk, hdim, vocab, chunk, 0) < fp32_sum
+    # one chunk or two: no fp32 sum
+    assert w(2 * chunk, hdim, vocab, chunk, 1) - w(2 * chunk, hdim, vocab, chunk, 0) < fp32_sum
+
+
 def test_plan_sizes(lib):
     assert lib.siq_attn_plan_bytes(-1, 10, 10) == 0
     a, b = lib.siq_attn_plan_bytes(32, 16384, 16384), lib.siq_attn_plan_bytes(200, 32768, 32768)
