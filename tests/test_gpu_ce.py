@@ -115,6 +115,25 @@ def test_qwen_vocab_vs_oracle():
     assert rel(dh, ref["dh"]) <= TOL and rel(dw, ref["dw"]) <= TOL
 
 
+def test_vocab_past_one_factor_segment_vs_oracle():
+    """V = 270000: 1055 vocab tiles, more than the row pass keeps factors for
+    at once (1024), so it streams each row in two segments; the last tile
+    holds 176 columns.  Two chunks, so dW is also summed over chunks."""
+    h, w, y = make(96, 64, 270000, seed=9, wscale=0.05)
+    y[7] = 269999  # the last column of the partial last tile
+    y[8] = 262143  # the last column of the first segment
+    y[9] = 262144  # the first column of the second segment
+    print("flce vocab 270000 n=96 chunk=64", flush=True)
+    loss, count, _, dh, dw = run(h, w, y, 64)
+    ref = oc.linear_ce(h, w, y, block=32)
+    assert count == ref["count"]
+    assert abs(loss - ref["loss"]) <= TOL * abs(ref["loss"])
+    assert rel(dh, ref["dh"]) <= TOL and rel(dw, ref["dw"]) <= TOL
+    # the labelled columns' dW rows are dominated by the -g term: check them alone too
+    for v in (269999, 262143, 262144):
+        assert rel(dw[v], ref["dw"][v]) <= TOL, v
+
+
 def test_large_logits_keep_relative_precision():
     # logits of magnitude ~30: the exp-normalised chunk buffer keeps precision
     h, w, y = make(128, 256, 2048, seed=6, wscale=2.0)
