@@ -98,3 +98,15 @@ def test_tile_boundary_lengths(d):
     lengths = [63, 64, 65, 127, 128, 129, 1]
     check(lengths, lengths, 12, 2, d, True, seed=4)
     check(lengths, lengths, 4, 4, d, False, seed=5)
+
+
+@pytest.mark.parametrize("d,causal", [(128, True), (64, False)])
+def test_many_tiny_sequences(d, causal):
+    # 700 sequences of 0..24 tokens and one of 900: the schedule's q-tile and
+    # dK/dV item lists hold ~700 single-tile entries beside one heavy tile that
+    # is cut into pieces (a dropped or duplicated entry shows up as a wrong or
+    # zero row against the oracle)
+    g = np.random.default_rng(17)
+    lengths = [int(x) for x in g.integers(0, 25, size=700)]
+    lengths.insert(350, 900)
+    check(lengths, lengths, 4, 2, d, causal, seed=6)
