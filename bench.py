@@ -60,14 +60,46 @@ MIN_STEPS = 20
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
 
 
-def measured_traffic(key: str):
+CSRC_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "siq_vl_amd", "csrc")
+
+
+def kernel_sources_digest() -> str:
+    """sha256 (first 16 hex digits) over the kernel sources (file names and
+    contents, in name order): what profiles/traffic.json is stamped with when
+    the rocprofv3 passes are summarised, so that a traffic figure measured on
+    other kernels is recognised as stale."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(CSRC_DIR)):
+        path = os.path.join(CSRC_DIR, name)
+        if os.path.isfile(path) and name.endswith((".hip", ".h", ".cpp")):
+            h.update(name.encode())
+            with open(path, "rb") as fh:
+                h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(key: str) -> dict:
     """HBM bytes per call of ``key`` from the last rocprofv3 FETCH_SIZE / WRITE_SIZE
-    passes (scaled by a plain copy's readings), or None if never measured."""
+    passes (scaled by a plain copy's readings), with the commit and kernel
+    sources they were measured on.  ``bytes`` is None when never measured or
+    when the kernel sources changed since (``stale``)."""
+    out = {"bytes": None, "measured_at_commit": None, "stale": None}
     try:
         with open(TRAFFIC_FILE) as fh:
-            return int(json.load(fh)[key]["bytes_per_call"])
+            ent = json.load(fh)[key]
     except (OSError, KeyError, ValueError):
-        return None
+        return out
+    cur = kernel_sources_digest()
+    stale = ent.get("sources_sha16") != cur
+    out.update({"measured_at_commit": ent.get("commit"), "sources_sha16": ent.get("sources_sha16"),
+                "current_sources_sha16": cur, "stale": stale})
+    if stale:
+        out["stale_bytes"] = int(ent["bytes_per_call"])
+    else:
+        out["bytes"] = int(ent["bytes_per_call"])
+    return out
 
 
 METRIC = "packed varlen attn fwd+bwd TFLOP/s (% bf16 MFMA peak); fused-CE tokens/s"
@@ -481,7 +513,8 @@ def bench_splice(steps: int, warmup: int) -> dict:
                 fn()
         return timed(gr.replay, reps)
 
-    # the kernels alone (the op adds one device-to-host read of the count, as the reference's nonzero does)
+    # the kernels alone; the op adds the count check: lazy (a pinned copy and an event, judged at the next call)
+    # or sync (one device-to-host read, as the reference's nonzero makes)
     fwd_ms = graphed(lambda: SP.splice_fwd(flat, weight, vis, img))
 
     def ref_step():
@@ -489,11 +522,37 @@ def bench_splice(steps: int, warmup: int) -> dict:
         positions = (ids == img).nonzero(as_tuple=True)
         te[positions] = vis
 
+    def queued(fn):
+        """GPU time per call with the host running ahead (as in a training step): a spin kernel holds the
+        stream while the calls are enqueued behind it, so the events time the GPU, not the host."""
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ev = _events(steps + 1)
+        torch.cuda._sleep(40_000_000)
+        ev[0].record(stream)
+        for i in range(steps):
+            fn()
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+        return per[len(per) // 2]
+
     ref_ms = timed(ref_step, 1)
     op_ms = timed(lambda: SP.splice_vision_tokens(ids, weight, vis, img), 1)
+    op_sync_ms = timed(lambda: SP.splice_vision_tokens(ids, weight, vis, img, validate="sync"), 1)
+    op_queued_ms = queued(lambda: SP.splice_vision_tokens(ids, weight, vis, img))
+    SP.check_pending_splices(block=True)
+    # the embedding table's gradient (full fine-tune): the HIP per-id sum against torch's embedding backward
+    gout = torch.randn(n, hidden, generator=g).to(torch.bfloat16).to(dev)
+    table_ms = graphed(lambda: SP.embedding_bwd(gout, flat, vocab, (img,)), reps=5)
+    table_ref_ms = timed(lambda: torch.ops.aten.embedding_dense_backward(gout, flat, vocab, img, False), 1)
     nbytes = SP.splice_bytes(n, hidden)
-    return {"fwd_ms": fwd_ms, "op_ms": op_ms, "ref_ms": ref_ms, "bytes": nbytes,
-            "gbs": nbytes / (fwd_ms * 1e-3) / 1e9}
+    table_bytes = n * (hidden * 2 + 8) + vocab * hidden * 2
+    return {"fwd_ms": fwd_ms, "op_ms": op_ms, "op_sync_ms": op_sync_ms, "op_queued_ms": op_queued_ms,
+            "ref_ms": ref_ms, "bytes": nbytes,
+            "gbs": nbytes / (fwd_ms * 1e-3) / 1e9, "table_ms": table_ms, "table_ref_ms": table_ref_ms,
+            "table_bytes": table_bytes, "table_gbs": table_bytes / (table_ms * 1e-3) / 1e9}
 
 
 def bench_ce(steps: int, warmup: int, chunk: int | None) -> dict:
@@ -528,7 +587,34 @@ def _cpu_threads() -> int:
     return min(cores, int(os.environ.get("OMP_NUM_THREADS") or cores))
 
 
-def cpu_baseline(budget_s: float = 20.0) -> dict:
+def _cpu_attention_sample(cfg, lens: list[int], budget_s: float, max_reps: int = 50):
+    """fwd+bwd of the reference path (fp32 SDPA, block-diagonal mask,
+    repeat_kv, autograd) over ``lens``, each a prefix of the config's
+    sequences (the first len tokens of a causal sequence are themselves a
+    causal sequence).  Returns (TFLOP/s at 12 * d * P * Hq, reps)."""
+    from oracle import cpu_path
+
+    x = W.attn_inputs(cfg, device="cpu")
+    starts = cfg.cu_seqlens().tolist()
+    rows = torch.cat([torch.arange(starts[i], starts[i] + n) for i, n in lens])
+    q, k, v, do = (x[n][rows].float().requires_grad_(n != "dout") for n in ("q", "k", "v", "dout"))
+    cu = [0]
+    for _, n in lens:
+        cu.append(cu[-1] + n)
+    pairs = sum(n * (n + 1) // 2 for _, n in lens) if cfg.causal else sum(n * n for _, n in lens)
+    flops = 12.0 * cfg.d * pairs * cfg.hq
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        out = cpu_path.sdpa_attention(q, k, v, cu, cfg.d**-0.5, cfg.causal)
+        out.backward(do)
+        reps += 1
+        if time.perf_counter() - t0 > budget_s or reps >= max_reps:
+            break
+    return flops / ((time.perf_counter() - t0) / reps) / 1e12, reps
+
+
+def cpu_baseline(budget_s: float = 24.0) -> dict:
     """Reference path (oracle/cpu_path.py) on the host cores, bounded samples."""
     from oracle import cpu_path
 
@@ -537,30 +623,37 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
     # config 2 (headline): the first sequences of the batch, ~2048 tokens, fwd+bwd
     cfg = W.attn_config(2)
     lens = []
-    for n in cfg.lengths:
-        if sum(lens) + n > 2048 and lens:
+    for i, n in enumerate(cfg.lengths):
+        if sum(m for _, m in lens) + n > 2048 and lens:
             break
-        lens.append(n)
-    x = W.attn_inputs(cfg, device="cpu", total=sum(lens))
-    cu = [0]
-    for n in lens:
-        cu.append(cu[-1] + n)
-    q, k, v, do = (x[n].float().requires_grad_(n != "dout") for n in ("q", "k", "v", "dout"))
-    pairs = sum(n * (n + 1) // 2 for n in lens)
-    flops = 12.0 * cfg.d * pairs * cfg.hq
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        out = cpu_path.sdpa_attention(q, k, v, cu, cfg.d**-0.5, True)
-        out.backward(do)
-        reps += 1
-        if time.perf_counter() - t0 > budget_s * 0.4 or reps >= 50:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    res["attn"] = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-                   "kind": "port",
-                   "sample": f"config-2 first {len(lens)} sequences ({sum(lens)} tokens), fp32 SDPA + block-diagonal "
-                             f"mask + repeat_kv, fwd+bwd autograd, {reps} reps"}
+        lens.append((i, n))
+    tf, reps = _cpu_attention_sample(cfg, lens, budget_s * 0.25)
+    res["attn"] = {"value": tf, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+                   "sample": f"config-2 first {len(lens)} sequences ({sum(n for _, n in lens)} tokens), fp32 SDPA + "
+                             f"block-diagonal mask + repeat_kv, fwd+bwd autograd, {reps} reps"}
+    # config 3: two whole 1024-token images (16 heads, d 64, bidirectional)
+    c3 = W.attn_config(3)
+    tf, reps = _cpu_attention_sample(c3, [(0, 1024), (1, 1024)], budget_s * 0.15)
+    res["attn_config3"] = {"value": tf, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+                           "sample": f"config 3, 2 of the 16 images (2 x 1024 tokens, 16/16 heads, d 64), fp32 SDPA "
+                                     f"+ block-diagonal bidirectional mask, fwd+bwd autograd, {reps} reps"}
+    # config 5: the first 2048 tokens of the 16384-token sequence (a causal prefix) plus the first short
+    # sequences (81..600 tokens) up to ~1024 tokens
+    c5 = W.attn_config(5)
+    short = []
+    for i, n in enumerate(c5.lengths):
+        if n <= 600:
+            if sum(m for _, m in short) + n > 1024 and short:
+                break
+            short.append((i, n))
+    big = max(range(len(c5.lengths)), key=lambda i: c5.lengths[i])
+    lens5 = [(big, 2048)] + short
+    tf, reps = _cpu_attention_sample(c5, lens5, budget_s * 0.15)
+    res["attn_config5"] = {"value": tf, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+                           "sample": f"config 5, the first 2048 tokens of its 16384-token sequence plus {len(short)} "
+                                     f"of its short sequences ({sum(n for _, n in short)} tokens, 81..600 each), "
+                                     f"12/2 heads, d 128, fp32 SDPA + block-diagonal causal mask + repeat_kv, "
+                                     f"fwd+bwd autograd, {reps} reps"}
     # config 1 (CPU-reported in the baseline): the whole batch, forward only
     c1 = W.attn_config(1)
     x1 = W.attn_inputs(c1, device="cpu")
@@ -573,7 +666,7 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
         while True:
             cpu_path.sdpa_attention(q1, k1, v1, cu1, c1.d**-0.5, True)
             reps += 1
-            if time.perf_counter() - t0 > budget_s * 0.3 or reps >= 20:
+            if time.perf_counter() - t0 > budget_s * 0.2 or reps >= 20:
                 break
     dt1 = (time.perf_counter() - t0) / reps
     res["attn_config1"] = {"value": flops1 / dt1 / 1e12, "unit": "TFLOP/s", "ms": dt1 * 1e3,
@@ -593,7 +686,7 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
         loss = cpu_path.cross_entropy(h, w, y)
         loss.backward()
         reps += 1
-        if time.perf_counter() - t0 > budget_s * 0.3 or reps >= 20:
+        if time.perf_counter() - t0 > budget_s * 0.2 or reps >= 20:
             break
     dt = (time.perf_counter() - t0) / reps
     res["ce"] = {"value": n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
@@ -713,9 +806,10 @@ def main() -> int:
     spl = None
     if not args.skip_splice:
         spl = bench_splice(leg_steps, args.warmup)
-        print(f"[bench] splice kernels {spl['fwd_ms'] * 1e3:.1f} us ({spl['gbs']:.0f} GB/s), whole op with its count "
-              f"check {spl['op_ms'] * 1e3:.1f} us; reference torch ops {spl['ref_ms'] * 1e3:.1f} us",
-              file=sys.stderr, flush=True)
+        print(f"[bench] splice kernels {spl['fwd_ms'] * 1e3:.1f} us ({spl['gbs']:.0f} GB/s), whole op with its lazy "
+              f"count check {spl['op_ms'] * 1e3:.1f} us (host ahead {spl['op_queued_ms'] * 1e3:.1f} us, sync {spl['op_sync_ms'] * 1e3:.1f} us); reference torch ops "
+              f"{spl['ref_ms'] * 1e3:.1f} us; table gradient {spl['table_ms'] * 1e3:.1f} us "
+              f"({spl['table_gbs']:.0f} GB/s; torch {spl['table_ref_ms'] * 1e3:.1f} us)", file=sys.stderr, flush=True)
     clock_end = probe_clock_mhz()
     cpu = None if args.no_cpu_baseline else cpu_baseline()
 
@@ -724,6 +818,7 @@ def main() -> int:
     # kernels back to back, as rocprofv3 times them), in the default (deterministic) mode
     bwd_graph_ms = att["bwd_graph_ms_deterministic" if A.DETERMINISTIC_DEFAULT else "bwd_graph_ms_atomic"]
     bwd_achieved = att["flops_bwd"] / (bwd_graph_ms * 1e-3) / 1e12
+    traffic_bwd = measured_traffic("attention_bwd_config2")
     line = {
         "metric": METRIC,
         "value": round(att["tflops"], 3),
@@ -755,7 +850,7 @@ def main() -> int:
                      "duration_us": round(bwd_graph_ms * 1e3, 1),
                      "achieved": round(bwd_achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(bwd_achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": measured_traffic("attention_bwd_config2"),
+                     "traffic": traffic_bwd["bytes"], "traffic_source": traffic_bwd,
                      "algorithmic_bytes": att["bytes_bwd"]},
         "cpu_baseline": cpu["attn"] if cpu else None,
         "gpu_clock_mhz": {"after_headline": None if clock is None else round(clock, 1),
@@ -766,7 +861,10 @@ def main() -> int:
     }
     if cpu:
         line["attention_configs"]["1"]["cpu_baseline"] = cpu["attn_config1"]
+        line["attention_configs"]["3"]["cpu_baseline"] = cpu["attn_config3"]
+        line["attention_configs"]["5"]["cpu_baseline"] = cpu["attn_config5"]
     if ce is not None:
+        traffic_ce = measured_traffic("ce_config4")
         line["ce"] = {"workload": "config 4: fused linear CE fwd+bwd, h [16384,1536], W [151936,1536], 30% span mask",
                       "tokens_per_s": round(ce["tokens_per_s"], 1), "ms_per_step": round(ce["ms_per_step"], 4),
                       "mean_ms_per_step": round(ce["mean_ms_per_step"], 4),
@@ -779,7 +877,7 @@ def main() -> int:
                                    "achieved": round(ce["tflops_executed"], 2), "peak": PEAK_BF16_TFLOPS,
                                    "unit": "TFLOP/s", "frac": round(ce["tflops_executed"] / PEAK_BF16_TFLOPS, 4),
                                    "work": "6 * rows_with_label * hdim * vocab",
-                                   "traffic": measured_traffic("ce_config4"),
+                                   "traffic": traffic_ce["bytes"], "traffic_source": traffic_ce,
                                    "algorithmic_bytes": ce["algorithmic_bytes"]},
                       "cpu_baseline": cpu["ce"] if cpu else None}
     if rope is not None:
@@ -821,7 +919,19 @@ def main() -> int:
             "roofline": {"bound": "hbm", "achieved": round(spl["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(spl["gbs"] / PEAK_HBM_GBS, 4), "algorithmic_bytes": spl["bytes"]},
             "op_with_count_check_us": round(spl["op_ms"] * 1e3, 2),
-            "reference_torch_ops_us": round(spl["ref_ms"] * 1e3, 2)}
+            "op_with_count_check_host_ahead_us": round(spl["op_queued_ms"] * 1e3, 2),
+            "op_with_sync_count_check_us": round(spl["op_sync_ms"] * 1e3, 2),
+            "op_timing": "eager calls back to back (the host's launch work is on the clock); host_ahead: the calls "
+                         "queued behind a spin kernel, so the GPU's own time per call",
+            "reference_torch_ops_us": round(spl["ref_ms"] * 1e3, 2),
+            "table_gradient": {
+                "workload": "embedding-table gradient of the same 16384 tokens into [151936, 1536] bf16 (image "
+                            "token skipped)",
+                "us": round(spl["table_ms"] * 1e3, 2), "timing": "5 launches in a HIP graph, replayed",
+                "roofline": {"bound": "hbm", "achieved": round(spl["table_gbs"], 1), "peak": PEAK_HBM_GBS,
+                             "unit": "GB/s", "frac": round(spl["table_gbs"] / PEAK_HBM_GBS, 4),
+                             "algorithmic_bytes": spl["table_bytes"]},
+                "torch_embedding_dense_backward_us": round(spl["table_ref_ms"] * 1e3, 2)}}
     if cpu:
         line["host"] = cpu["host"]
     print(json.dumps(line), flush=True)

@@ -11,7 +11,7 @@
  *   4. the pixel-shuffle projector (vision features to text embeddings),
  *      forward and backward, with the shuffle folded into the GEMM loads;
  *   5. the splice of the projected vision rows into the token embeddings,
- *      fused with the embedding gather.
+ *      fused with the embedding gather, and its embedding-table gradient.
  *
  * Conventions
  *  - Every entry point returns an int status (SIQ_OK = 0, < 0 on error) and
@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define SIQ_ABI_VERSION 3
+#define SIQ_ABI_VERSION 4
 
 enum siq_status {
   SIQ_OK = 0,
@@ -324,7 +324,11 @@ int siq_proj_bwd(const void* x, const void* weight, const void* dy, void* dx, vo
  * siq_splice_workspace_bytes(n_tokens).
  *
  * siq_gather_rows: dst[i] = src[rows[i]], i < n (rows of hidden bf16): the
- * backward's vision-row gradient (IndexPutBackward of :270) from image_pos.
+ * backward's vision-row gradient (IndexPutBackward of :270) from image_pos;
+ * rows[i] < 0 gives a zero row (image_pos slots past the image tokens found
+ * hold -1).  The splice and the gather only copy 16-byte chunks of rows, so
+ * rows of another dtype are passed as their bf16 view (an fp32 row of H
+ * elements as 2H bf16).
  * ------------------------------------------------------------------------- */
 size_t siq_splice_workspace_bytes(int64_t n_tokens);
 
@@ -333,6 +337,32 @@ int siq_splice_fwd(const int64_t* input_ids, int64_t n_tokens, const void* weigh
                    int64_t* counts, void* workspace, size_t workspace_bytes, void* stream);
 
 int siq_gather_rows(const void* src, const int32_t* rows, int64_t n, int64_t hidden, void* dst, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Embedding-table gradient of the splice (the text model's input embeddings).
+ *
+ * Replaces the backward of the embedding lookup at siq_vl/model/modeling.py:253
+ * together with the index assignment at :270 (IndexPutBackward zeroes the
+ * overwritten image rows before the embedding backward): torch's
+ * embedding_dense_backward with the image token as padding index.
+ *   dweight[v] = sum of grad[p] over tokens p with input_ids[p] == v,
+ * for v in [0, vocab) other than skip_id0 / skip_id1 (the image token and the
+ * table's padding index; -1 for none); every other row is zero.  The sum is
+ * fp32, in the order of torch's sorted embedding backward (each id's tokens
+ * in position order, partial sums of at most 10 rows added in order), rounded
+ * once; deterministic.  grad [n_tokens, hidden] and dweight [vocab, hidden]
+ * contiguous, 16-byte aligned, both bf16 (dtype SIQ_DTYPE_BF16) or both fp32
+ * (SIQ_DTYPE_FP32, the reference's fp32 master weights); hidden % 8 == 0.
+ * Workspace: siq_embedding_bwd_workspace_bytes(n_tokens, vocab).
+ * ------------------------------------------------------------------------- */
+#define SIQ_DTYPE_BF16 0
+#define SIQ_DTYPE_FP32 1
+
+size_t siq_embedding_bwd_workspace_bytes(int64_t n_tokens, int64_t vocab);
+
+int siq_embedding_bwd(const void* grad, const int64_t* input_ids, int64_t n_tokens, int64_t vocab, int64_t hidden,
+                      int dtype, int64_t skip_id0, int64_t skip_id1, void* dweight, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Measurement support (no reference counterpart).

@@ -99,6 +99,9 @@ _PROTOS = {
     "siq_splice_fwd": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
                               _c_void_p, _c_void_p, _size, _c_void_p]),
     "siq_gather_rows": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
+    "siq_embedding_bwd_workspace_bytes": (_size, [_i64, _i64]),
+    "siq_embedding_bwd": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _i64, _i64, _c_void_p, _c_void_p,
+                                 _size, _c_void_p]),
     "siq_probe_clock": (_i32, [_c_void_p, _i64, _c_void_p]),
     "siq_rope_fwd": (
         _i32,

@@ -133,17 +133,40 @@ class AttnPlan:
     sequences, the head counts and causality, so one plan serves the forward
     and backward of every layer of a packed batch (the reference forwards the
     same ``cu_seq_lens_*`` kwargs to each decoder layer,
-    siq_vl/model/modeling.py:278-288)."""
+    siq_vl/model/modeling.py:278-288).
 
-    __slots__ = ("buf", "batch", "total_q", "total_k", "hq", "hkv", "causal", "cu_q", "cu_k", "__weakref__")
+    ``cu_q`` / ``cu_k`` are the plan's own device copies of the offsets it was
+    built from (nothing else holds them, so they cannot change under it);
+    ``src`` remembers the caller's tensors and their versions, so that handing
+    the same unchanged tensors back with the plan needs no comparison."""
 
-    def __init__(self, buf, batch, total_q, total_k, hq, hkv, causal, cu_q, cu_k):
+    __slots__ = ("buf", "batch", "total_q", "total_k", "hq", "hkv", "causal", "cu_q", "cu_k", "src", "__weakref__")
+
+    def __init__(self, buf, batch, total_q, total_k, hq, hkv, causal, cu_q, cu_k, src=()):
         self.buf, self.batch, self.total_q, self.total_k = buf, batch, total_q, total_k
         self.hq, self.hkv, self.causal, self.cu_q, self.cu_k = hq, hkv, causal, cu_q, cu_k
+        self.src = src
 
     def matches(self, batch: int, total_q: int, total_k: int, hq: int, hkv: int, causal: bool) -> bool:
         return (self.batch, self.total_q, self.total_k, self.hq // self.hkv, self.hkv, self.causal) == (
             batch, total_q, total_k, hq // hkv, hkv, bool(causal))
+
+    def describes(self, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor) -> bool:
+        """True when the plan was built from these offsets: the plan's own
+        copies, the unchanged tensors it was built from, or tensors holding
+        the same values (compared on the device: one device-to-host read)."""
+        for given, own, i in ((cu_seqlens_q, self.cu_q, 0), (cu_seqlens_k, self.cu_k, 1)):
+            if given is own:
+                continue
+            if len(self.src) == 2:
+                ref, ver = self.src[i]
+                if ref() is given and given._version == ver:
+                    continue
+            if given.dim() != 1 or given.numel() != own.numel():
+                return False
+            if not torch.equal(given.to(device=own.device, dtype=torch.int32), own):
+                return False
+        return True
 
     def status(self) -> dict:
         """The plan header's status words (one device-to-host read; for tests
@@ -153,12 +176,21 @@ class AttnPlan:
         return {"magic": words[4], "status_q": words[10], "status_kv": words[11], "status_use": words[12]}
 
 
+def _own_copy(src: torch.Tensor, dev_copy: torch.Tensor) -> torch.Tensor:
+    """A device copy of offsets that no caller holds (``dev_copy`` itself when
+    it was made from a host tensor, else a clone)."""
+    return dev_copy if dev_copy is not src else dev_copy.clone()
+
+
 def build_attn_plan(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, total_q: int, total_k: int, hq: int,
                     hkv: int, causal: bool, device: torch.device | None = None) -> AttnPlan:
     """Builds a plan on the device (one small kernel, no host sync)."""
     device = _norm_device(device or (cu_seqlens_q.device if cu_seqlens_q.device.type == "cuda" else "cuda"))
-    cu_q = _device_cu(cu_seqlens_q, device, total_q, "cu_seqlens_q")
-    cu_k = _device_cu(cu_seqlens_k, device, total_k, "cu_seqlens_k")
+    cu_q = _own_copy(cu_seqlens_q, _device_cu(cu_seqlens_q, device, total_q, "cu_seqlens_q"))
+    if cu_seqlens_k is cu_seqlens_q:
+        cu_k = cu_q
+    else:
+        cu_k = _own_copy(cu_seqlens_k, _device_cu(cu_seqlens_k, device, total_k, "cu_seqlens_k"))
     if cu_q.numel() != cu_k.numel():
         raise ValueError("cu_seqlens_q and cu_seqlens_k must describe the same number of sequences")
     if hq <= 0 or hkv <= 0 or hq % hkv:
@@ -171,7 +203,8 @@ def build_attn_plan(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, tota
         rc = L.siq_attn_build_plan(cu_q.data_ptr(), cu_k.data_ptr(), batch, total_q, total_k, hq, hkv,
                                    int(bool(causal)), buf.data_ptr(), buf.numel(), _stream(device))
         _lib.check(rc, "siq_attn_build_plan")
-    return AttnPlan(buf, batch, int(total_q), int(total_k), int(hq), int(hkv), bool(causal), cu_q, cu_k)
+    src = tuple((weakref.ref(t), t._version) for t in (cu_seqlens_q, cu_seqlens_k))
+    return AttnPlan(buf, batch, int(total_q), int(total_k), int(hq), int(hkv), bool(causal), cu_q, cu_k, src)
 
 
 _PLAN_ATTR = "_siq_attn_plans"
@@ -206,8 +239,11 @@ def cached_attn_plan(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, tot
 def _resolve_plan(plan, cu_seqlens_q, cu_seqlens_k, total_q, total_k, hq, hkv, causal, device) -> AttnPlan:
     if plan is None:
         return cached_attn_plan(cu_seqlens_q, cu_seqlens_k, total_q, total_k, hq, hkv, causal, device)
-    if not plan.matches(plan.batch, total_q, total_k, hq, hkv, causal) or plan.buf.device != _norm_device(device):
+    batch = cu_seqlens_q.numel() - 1
+    if not plan.matches(batch, total_q, total_k, hq, hkv, causal) or plan.buf.device != _norm_device(device):
         raise ValueError("the attention plan was built for other sequences, heads or causality")
+    if not plan.describes(cu_seqlens_q, cu_seqlens_k):
+        raise ValueError("the attention plan was built for other sequences (cu_seqlens differ from the plan's)")
     return plan
 
 

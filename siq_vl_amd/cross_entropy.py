@@ -10,17 +10,17 @@ holds more than one token chunk of (exp-normalised) logits, bounded at
 ``DEFAULT_E_BUDGET_BYTES``.
 
 The forward computes the loss and both gradients at once; the backward only
-rescales them by the upstream gradient (a device scalar, no host sync).
+rescales them by the upstream gradient (a device scalar, no host sync), in
+place unless the graph is retained.
 Without gradients (evaluation) the loss-only ``siq_flce_loss`` runs.
 """
 
 from __future__ import annotations
 
-import threading
-
 import torch
 
 from . import _lib
+from ._deferred import DeferredChecks
 
 IGNORE_INDEX = -100
 # Bound on the one logits-sized buffer, a token chunk's softmax numerators
@@ -140,8 +140,7 @@ class LabelError(ValueError):
 # host memory without blocking and checked when the copy has landed: at the
 # next call, or when check_pending_labels() is called.  validate="sync" reads it
 # at once (one device-to-host sync), validate=False never checks.
-_PENDING: list = []
-_PENDING_LOCK = threading.Lock()
+_LABEL_CHECKS = DeferredChecks()
 
 
 def _raise_bad(nbad: int, vocab: int, ignore_index: int) -> None:
@@ -152,43 +151,46 @@ def _raise_bad(nbad: int, vocab: int, ignore_index: int) -> None:
 def check_pending_labels(block: bool = False) -> None:
     """Raises LabelError for any earlier call whose bad-label count has landed
     and is non-zero (all of them when ``block``)."""
-    with _PENDING_LOCK:
-        keep = []
-        found = None
-        for ev, host, vocab, ign in _PENDING:
-            if block:
-                ev.synchronize()
-            if ev.query():
-                if int(host) > 0 and found is None:
-                    found = (int(host), vocab, ign)
-            else:
-                keep.append((ev, host, vocab, ign))
-        _PENDING[:] = keep
-    if found is not None:
-        _raise_bad(*found)
+    _LABEL_CHECKS.check(block)
 
 
 def _track_bad(bad: torch.Tensor, vocab: int, ignore_index: int, validate) -> None:
     if validate is False or validate is None:
+        return
+    if torch.cuda.is_current_stream_capturing():
+        # Inside HIP graph capture neither a host read nor an event query of
+        # earlier work is allowed: the labels of a captured call are not
+        # validated (check them once outside the graph, with validate="sync").
         return
     if validate == "sync":
         nbad = int(bad)
         if nbad > 0:
             _raise_bad(nbad, vocab, ignore_index)
         return
-    check_pending_labels()
-    host = torch.empty((), dtype=torch.int64, pin_memory=True)
-    host.copy_(bad, non_blocking=True)
-    ev = torch.cuda.Event()
-    ev.record(torch.cuda.current_stream(bad.device))
-    with _PENDING_LOCK:
-        _PENDING.append((ev, host, vocab, ignore_index))
+
+    def judge(vals):
+        if vals[0] > 0:
+            _raise_bad(int(vals[0]), vocab, ignore_index)
+
+    _LABEL_CHECKS.add(bad, judge)
 
 
-def _scaled(t: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
-    """t * g as a new bf16 tensor (the saved gradients stay untouched, so a
-    second backward through a retained graph sees them unscaled)."""
-    out = torch.empty_like(t)
+def _keeps_graph() -> bool:
+    """True inside a backward that retains the graph (``retain_graph=True``):
+    the saved gradients must then survive it.  Unknown (a torch without the
+    query) counts as True, the safe side."""
+    try:
+        return bool(torch._C._autograd._get_current_graph_task_keep_graph())
+    except (AttributeError, RuntimeError):
+        return True
+
+
+def _scaled(t: torch.Tensor, g: torch.Tensor, inplace: bool) -> torch.Tensor:
+    """t * g in bf16: in place (the saved gradient becomes the returned one,
+    no second [vocab, hdim] buffer at the backward's peak), or into a new
+    tensor when the graph is retained, so that a second backward sees the
+    saved gradients unscaled."""
+    out = t if inplace else torch.empty_like(t)
     rc = _lib.lib().siq_scale_bf16(t.data_ptr(), out.data_ptr(), t.numel(), g.data_ptr(),
                                    torch.cuda.current_stream(t.device).cuda_stream)
     _lib.check(rc, "siq_scale_bf16")
@@ -215,8 +217,9 @@ class _FusedLinearCE(torch.autograd.Function):
     def backward(ctx, grad_loss):
         dh, dw = ctx.saved_tensors
         g = grad_loss.detach().to(torch.float32).reshape(()).contiguous()
-        gh = _scaled(dh, g).reshape(ctx.shape) if ctx.needs_input_grad[0] else None
-        gw = _scaled(dw, g) if ctx.has_dw and ctx.needs_input_grad[1] else None
+        inplace = not _keeps_graph()
+        gh = _scaled(dh, g, inplace).reshape(ctx.shape) if ctx.needs_input_grad[0] else None
+        gw = _scaled(dw, g, inplace) if ctx.has_dw and ctx.needs_input_grad[1] else None
         return gh, gw, None, None, None, None, None
 
 
@@ -235,7 +238,14 @@ def fused_linear_cross_entropy(hidden: torch.Tensor, weight: torch.Tensor, label
     Labels outside ``[0, vocab)`` other than ``ignore_index`` raise
     ``LabelError``: ``validate="lazy"`` (default) without a host sync, at the
     next call or ``check_pending_labels()``; ``"sync"`` at once; ``False``
-    never.
+    never.  A lazy check of the last call surfaces only at a later call, so a
+    training or evaluation loop ends with ``check_pending_labels(block=True)``.
+    Calls captured in a HIP graph are not validated (no host work is allowed
+    there).
+
+    ``weight`` that does not require grad (a frozen ``lm_head``: the
+    reference's stage 1, and stage 2's LoRA, which leaves ``lm_head`` out of
+    its targets) gives the dH-only call: no dW GEMM and no dW buffer.
     """
     divisor = None
     if num_items_in_batch is not None:

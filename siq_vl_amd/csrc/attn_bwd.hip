@@ -676,11 +676,12 @@ struct DkvSum {
   static_assert(kBwdBN % ROWS == 0, "rows split evenly");
 };
 
-template <int D>
+template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_sum_kernel(const AttnParams p) {
   using S = DkvSum<D>;
   constexpr int BN = kBwdBN;
-  if (!plan_matches(p, p.plan->causal != 0, true)) return;
+  // the call's own causality: a plan built for the other one leaves dK / dV alone here too
+  if (!plan_matches(p, CAUSAL, true)) return;
   const int units = *p.nsplit * S::NCH;
   for (int unit = blockIdx.x; unit < units; unit += gridDim.x) {
   const int tile = unit / S::NCH, ch = unit % S::NCH;
@@ -959,10 +960,12 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const AttnParams p) 
   }
 }
 
-// Atomic backward, last: dq = bf16(scale * dQ sums).
-template <int D>
+// Atomic backward, last: dq = bf16(scale * dQ sums).  Checks the plan like
+// the other kernels, so a mismatched call leaves dq alone.
+template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_bwd_dq_convert_kernel(const AttnParams p) {
   constexpr int LP = D / 8, PPB = 256 / LP;
+  if (!plan_matches(p, CAUSAL, true)) return;
   const int sub = threadIdx.x % LP;
   const int64_t npairs = p.total_q * p.hq;
   for (int64_t pi = (int64_t)blockIdx.x * PPB + threadIdx.x / LP; pi < npairs; pi += (int64_t)gridDim.x * PPB) {
@@ -990,10 +993,10 @@ hipError_t launch_bwd_t(const AttnParams& p, int qcap, int kvcap, hipStream_t st
     const int64_t blocks = std::min<int64_t>((pairs + 256 / (D / 8) - 1) / (256 / (D / 8)), 8192);
     if (pblocks > 0) hipLaunchKernelGGL((attn_bwd_prep_kernel<D>), dim3((unsigned)pblocks), dim3(256), 0, stream, p);
     hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL, true>), kvgrid, dim3(512), 0, stream, p);
-    hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D>), dim3(min(kMaxSplitTiles * DkvSum<D>::NCH, 512), p.hkv), dim3(256),
+    hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D, CAUSAL>), dim3(min(kMaxSplitTiles * DkvSum<D>::NCH, 512), p.hkv), dim3(256),
                        0, stream, p);
     if (blocks > 0)
-      hipLaunchKernelGGL((attn_bwd_dq_convert_kernel<D>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((attn_bwd_dq_convert_kernel<D, CAUSAL>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
     return hipGetLastError();
   }
   // dQ first: it also writes Delta and LSE2, which the dK/dV kernel reads
@@ -1009,7 +1012,7 @@ hipError_t launch_bwd_t(const AttnParams& p, int qcap, int kvcap, hipStream_t st
     hipLaunchKernelGGL((attn_bwd_dkdv_w4_kernel<D, CAUSAL>), kvgrid, dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL, false>), kvgrid, dim3(512), 0, stream, p);
-  hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D>), dim3(min(kMaxSplitTiles * DkvSum<D>::NCH, 512), p.hkv), dim3(256), 0, stream,
+  hipLaunchKernelGGL((attn_bwd_dkv_sum_kernel<D, CAUSAL>), dim3(min(kMaxSplitTiles * DkvSum<D>::NCH, 512), p.hkv), dim3(256), 0, stream,
                      p);
   return hipGetLastError();
 }

@@ -735,6 +735,32 @@ int siq_gather_rows(const void* src, const int32_t* rows, int64_t n, int64_t hid
   return ok();
 }
 
+size_t siq_embedding_bwd_workspace_bytes(int64_t n_tokens, int64_t vocab) {
+  if (n_tokens < 0 || vocab <= 0) return 0;
+  return siq::embedding_bwd_workspace_bytes(n_tokens, vocab);
+}
+
+int siq_embedding_bwd(const void* grad, const int64_t* input_ids, int64_t n_tokens, int64_t vocab, int64_t hidden,
+                      int dtype, int64_t skip_id0, int64_t skip_id1, void* dweight, void* ws, size_t ws_bytes,
+                      void* stream) {
+  if (n_tokens < 0 || n_tokens >= (int64_t(1) << 31)) return fail(SIQ_ERR_INVALID_ARGUMENT, "n_tokens must be in [0, 2^31)");
+  if (vocab <= 0 || vocab >= (int64_t(1) << 31)) return fail(SIQ_ERR_INVALID_ARGUMENT, "vocab must be in [1, 2^31)");
+  if (hidden <= 0 || hidden % 8 != 0)
+    return fail(SIQ_ERR_UNSUPPORTED, "hidden (%lld) must be a positive multiple of 8", (long long)hidden);
+  if (dtype != SIQ_DTYPE_BF16 && dtype != SIQ_DTYPE_FP32)
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "dtype must be SIQ_DTYPE_BF16 or SIQ_DTYPE_FP32");
+  if (dweight == nullptr || !aligned16(dweight)) return fail(SIQ_ERR_ALIGNMENT, "dweight must be non-NULL and 16-byte aligned");
+  if (n_tokens > 0 && (grad == nullptr || input_ids == nullptr || !aligned16(grad)))
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "grad (16-byte aligned) and input_ids must not be NULL");
+  const size_t need = siq_embedding_bwd_workspace_bytes(n_tokens, vocab);
+  if (ws == nullptr || ws_bytes < need || !aligned16(ws))
+    return fail(SIQ_ERR_WORKSPACE, "workspace needs %zu bytes (16-byte aligned), got %zu", need, ws_bytes);
+  const hipError_t e = siq::embedding_bwd(grad, input_ids, n_tokens, vocab, hidden, dtype == SIQ_DTYPE_FP32, skip_id0,
+                                          skip_id1, dweight, ws, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "embedding backward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 int siq_scale_bf16_inplace(void* data, int64_t numel, const float* scalar, void* stream) {
   return siq_scale_bf16(data, data, numel, scalar, stream);
 }

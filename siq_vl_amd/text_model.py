@@ -67,9 +67,16 @@ def fused_causal_lm_forward(self, input_ids=None, attention_mask=None, position_
 def enable_fused_cross_entropy(model: torch.nn.Module, chunk_tokens: int | None = None) -> torch.nn.Module:
     """Routes ``model``'s loss through the fused kernel (in place); returns the
     module whose forward was replaced.  For ``SiQ_VLForCausalLM`` the text
-    model (``model.text_model``) is patched.  ``chunk_tokens`` None keeps the
-    default bound on the logits chunk."""
+    model (``model.text_model``) is patched, and when that is a PEFT wrapper
+    (``get_base_model()``), the causal LM inside it.  ``chunk_tokens`` None
+    keeps the default bound on the logits chunk."""
     target = getattr(model, "text_model", model)
+    # The reference's stage 2 with LoRA replaces text_model by a PEFT wrapper
+    # (siq_vl/model/modeling.py:388).  The wrapper's forward ends in the
+    # wrapped model's own ``forward`` attribute, so that model is patched.
+    get_base_model = getattr(target, "get_base_model", None)
+    if callable(get_base_model):
+        target = get_base_model()
     if not hasattr(target, "lm_head") or not hasattr(target, "model"):
         raise TypeError("expected a causal LM with .model (decoder) and .lm_head")
     target.siq_ce_chunk_tokens = None if chunk_tokens is None else int(chunk_tokens)

@@ -143,6 +143,43 @@ def test_large_logits_keep_relative_precision():
     assert rel(dh, ref["dh"]) <= TOL and rel(dw, ref["dw"]) <= TOL
 
 
+@pytest.mark.parametrize("n,hdim,vocab,chunk", [(300, 256, 1000, 128), (300, 256, 1000, 4096),
+                                                (256, 1536, W.QWEN_VOCAB, 4096)])
+def test_dh_only_vs_oracle(n, hdim, vocab, chunk):
+    """The call of a frozen lm_head (dweight = NULL: the reference's stage 1,
+    siq_vl/model/modeling.py:329-330, and stage 2's LoRA, which leaves lm_head
+    out of its targets, :377-386): loss and dH against the oracle, ignored
+    rows exactly zero, and bitwise the loss and dH of the call that also
+    forms dW."""
+    h, w, y = make(n, hdim, vocab, seed=21, wscale=0.05 if vocab < 4096 else 0.02)
+    y[5] = vocab + 1  # out of range: counted as bad, treated as ignored
+    print(f"flce dH only n={n} V={vocab} chunk={chunk}", flush=True)
+    loss, count, bad, dh, dw = run(h, w, y, chunk, need_dw=False)
+    assert dw is None
+    ref = oc.linear_ce(h, w, y, block=64)
+    assert count == ref["count"] and bad == ref["bad"] == 1
+    assert abs(loss - ref["loss"]) <= TOL * abs(ref["loss"])
+    assert rel(dh, ref["dh"]) <= TOL
+    ignored = ((y == -100) | (y >= vocab)).numpy()
+    assert np.all(dh[ignored] == 0.0)
+    both = run(h, w, y, chunk, need_dw=True)
+    assert both[0] == loss and np.array_equal(both[3], dh)
+
+
+def test_frozen_lm_head_autograd_takes_the_dh_only_call():
+    """hidden requires grad, the weight does not: the autograd op forms no dW
+    and hidden's gradient is the raw dH-only call's, scaled."""
+    h, w, y = make(200, 128, 768, seed=22)
+    hg = h.to(DEV).requires_grad_(True)
+    wd = w.to(DEV)
+    loss = C.fused_linear_cross_entropy(hg, wd, y.to(DEV), chunk_tokens=64)
+    (2.0 * loss).backward()
+    assert wd.grad is None
+    _, _, _, dh, dw = run(h, w, y, 64, need_dw=False)
+    assert dw is None
+    assert np.array_equal(hg.grad.float().cpu().numpy(), (torch.from_numpy(dh) * 2.0).to(torch.bfloat16).float().numpy())
+
+
 def test_autograd_matches_raw_and_scales():
     h, w, y = make(96, 128, 512, seed=8)
     hg = h.to(DEV).requires_grad_(True)
@@ -156,10 +193,16 @@ def test_autograd_matches_raw_and_scales():
 
 @pytest.mark.slow
 def test_full_size_vs_torch_fp32():
+    """Config 4 at full size, both the training call (dH and dW) and the
+    frozen-lm_head call (dH only), against one fp32 torch reference."""
     cfg = W.CONFIG4
     print(f"flce full size n={cfg.n} hdim={cfg.hdim} V={cfg.vocab}", flush=True)
     x = W.ce_inputs(cfg, device=DEV)
     loss, count, bad, dh, dw = C.flce_fwd_bwd(x["hidden"], x["weight"], x["labels"])
+    loss_h, count_h, bad_h, dh_h, dw_h = C.flce_fwd_bwd(x["hidden"], x["weight"], x["labels"], need_dweight=False)
+    assert dw_h is None and int(count_h) == int(count) and int(bad_h) == int(bad)
+    assert float(loss_h) == float(loss) and torch.equal(dh_h, dh)
+    del dh_h
     hf = x["hidden"].float()
     wf = x["weight"].float()
     y = x["labels"]

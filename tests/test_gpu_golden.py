@@ -61,3 +61,7 @@ def test_cross_entropy_golden():
         assert rel(dw.float().cpu().numpy(), f["dw"]) <= TOL
         zero_rows = np.all(f["dh"] == 0, axis=1)
         assert zero_rows.sum() > 0 and np.all(dh_np[zero_rows] == 0.0)
+        # the frozen-lm_head call (no dW): the same loss and dH
+        loss2, count2, _, dh2, dw2 = C.flce_fwd_bwd(h, w, y, -100, None, False, chunk)
+        assert dw2 is None and int(count2) == int(f["count"])
+        assert float(loss2) == float(loss) and torch.equal(dh2, dh)

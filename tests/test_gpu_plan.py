@@ -163,6 +163,62 @@ def test_mismatched_plan_writes_nothing_and_flags():
         A.varlen_attn_fwd(q, k4, v4, cu, cu, 200, 200, 128**-0.5, True, plan=plan)
 
 
+@pytest.mark.parametrize("deterministic", [True, False])
+def test_backward_with_plan_of_other_causality_writes_nothing(deterministic):
+    """A causal plan handed to a bidirectional backward through the C ABI, on
+    config 2's sequences (heavy kv tiles are split, so the partial-sum kernel
+    runs): every backward kernel -- dQ, dK/dV, the split-tile sum, the atomic
+    mode's dq conversion -- compares the plan with the call, leaves dq / dk /
+    dv at their fill value and flags the mismatch."""
+    cfg = W.attn_config(2)
+    lengths = cfg.lengths
+    print(f"mismatched-causality backward deterministic={deterministic}", flush=True)
+    q, k, v, do, cu = make(lengths, 12, 2, 128)
+    total = q.shape[0]
+    plan = A.build_attn_plan(cu, cu, total, total, 12, 2, True)
+    out, lse = A.varlen_attn_fwd(q, k, v, cu, cu, 0, 0, 128**-0.5, True, plan=plan)
+    dq, dk, dv = (torch.full_like(t, 3.0) for t in (q, k, v))
+    L = _lib.lib()
+    det = int(deterministic)
+    ws = torch.empty(L.siq_attn_bwd_plan_workspace_bytes(plan.batch, total, total, 12, 2, 128, det),
+                     dtype=torch.uint8, device=DEV)
+    st = _lib.int64_array([q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+                           out.stride(0), out.stride(1), do.stride(0), do.stride(1), dq.stride(0), dq.stride(1),
+                           dk.stride(0), dk.stride(1), dv.stride(0), dv.stride(1)])
+    rc = L.siq_attn_varlen_bwd_plan(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                    do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), plan.batch, total,
+                                    total, 12, 2, 128, st, 128**-0.5, 0, det, plan.buf.data_ptr(), plan.buf.numel(),
+                                    ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    for t in (dq, dk, dv):
+        assert bool((t == 3.0).all())
+    assert plan.status()["status_use"] == 2
+
+
+def test_plan_of_other_offsets_with_equal_totals_is_refused():
+    """Two packed batches with the same total and sequence count but other
+    lengths: a plan built for one is refused for the other (the host compares
+    the offsets), and accepted for tensors that hold its own offsets."""
+    a, b = [100, 300, 200], [300, 100, 200]
+    q, k, v, do, cu_a = make(a, 12, 2, 128)
+    cu_b = make(b, 12, 2, 128)[4]
+    plan = A.build_attn_plan(cu_a, cu_a, 600, 600, 12, 2, True)
+    with pytest.raises(ValueError, match="cu_seqlens"):
+        A.varlen_attn_fwd(q, k, v, cu_b, cu_b, 300, 300, 128**-0.5, True, plan=plan)
+    out, lse = A.varlen_attn_fwd(q, k, v, cu_a, cu_a, 300, 300, 128**-0.5, True, plan=plan)
+    with pytest.raises(ValueError, match="cu_seqlens"):
+        A.varlen_attn_bwd(do, q, k, v, out, lse, cu_b, cu_b, 300, 300, 128**-0.5, True, plan=plan)
+    # a copy of the same offsets (another tensor object, also on the CPU) is accepted
+    ref = A.varlen_attn_fwd(q, k, v, cu_a.clone(), cu_a.cpu(), 300, 300, 128**-0.5, True, plan=plan)
+    assert torch.equal(ref[0], out)
+    # an in-place change of the tensor the plan was built from is seen
+    cu_a[1] = 300
+    cu_a[2] = 400
+    with pytest.raises(ValueError, match="cu_seqlens"):
+        A.varlen_attn_fwd(q, k, v, cu_a, cu_a, 300, 300, 128**-0.5, True, plan=plan)
+
+
 def test_position_ids_offsets_computed_once():
     pos = torch.cat([torch.arange(n) for n in (5, 9, 2)]).reshape(1, -1).to(DEV)
     cu1, m1 = A._cu_from_position_ids(pos)

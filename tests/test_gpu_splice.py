@@ -2,10 +2,14 @@
 
 Bar: the splice only copies rows, so its output and the vision-row gradient
 are bitwise those of the reference's torch ops (embedding, nonzero, index
-assignment, autograd); the embedding table's gradient too.  End to end, a
+assignment, autograd), for bf16 and fp32 tables; the embedding table's
+gradient is one rounding of the exact per-id sum, deterministic, and bitwise
+torch's own where torch takes its sorted path.  End to end, a
 small model assembled like SiQ_VLForCausalLM (SigLIP tower -> pixel-shuffle
 projector -> splice -> Qwen2 decoder with labels) gives bitwise the stock
-logits and gradients with the splice alone patched; with every fused operator
+logits and gradients with the splice alone patched (the embedding table's
+within 1e-2: torch sums a short batch in another order, rounding to bf16 in
+between); with every fused operator
 of this package on (bf16) its loss stays within 2e-2 and every parameter
 gradient within 5e-2 of the stock fp32 model's.
 """
@@ -30,18 +34,21 @@ def bits(t):
     return t.detach().contiguous().view(torch.int16).cpu()
 
 
-def make(b, s, vocab, hidden, n_img_rows, seed=0, padding_idx=None):
+def make(b, s, vocab, hidden, n_img_rows, seed=0, padding_idx=None, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
     ids = torch.randint(0, vocab, (b, s), generator=g)
     ids[ids == IMG] = 1
     flat = ids.view(-1)
     pos = torch.randperm(flat.numel(), generator=g)[:n_img_rows]
     flat[pos] = IMG
+    if padding_idx is not None:
+        flat[torch.randperm(flat.numel(), generator=g)[:5]] = padding_idx  # some padding tokens too
+        flat[pos] = IMG
     emb = torch.nn.Embedding(vocab, hidden, padding_idx=padding_idx)
     with torch.no_grad():
         emb.weight.copy_(torch.randn(vocab, hidden, generator=g))
     vis = torch.randn(n_img_rows, hidden, generator=g)
-    return ids.to(DEV), emb.to(DEV).to(torch.bfloat16), vis.to(torch.bfloat16).to(DEV)
+    return ids.to(DEV), emb.to(DEV).to(dtype), vis.to(torch.bfloat16).to(DEV)
 
 
 def reference(ids, emb, vis):
@@ -52,26 +59,55 @@ def reference(ids, emb, vis):
     return te
 
 
-@pytest.mark.parametrize("shape", [(1, 1, 0), (2, 37, 9), (3, 300, 256), (1, 4096, 1024)])
+def table_grad_oracle(g, ids, vocab, padding_idx):
+    """fp64 per-id sum (the oracle's splice_bwd) of the upstream gradient."""
+    dw, _ = osp.splice_bwd(g.double().cpu().numpy(), ids.cpu().numpy(), IMG, vocab, padding_idx)
+    return dw
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 0), (2, 37, 9), (3, 300, 256), (1, 4096, 1024), (2, 9000, 512)])
 @pytest.mark.parametrize("padding_idx", [None, 0])
-def test_forward_backward_bitwise(shape, padding_idx):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_forward_backward(shape, padding_idx, dtype):
+    """Forward and the vision rows' gradient bitwise torch's ops (the splice
+    copies rows); the table's gradient within one rounding of the fp64 per-id
+    sum, deterministic, and bitwise torch's own embedding backward where torch
+    takes its sorted path (more than 3072 tokens), whose summation order the
+    kernel follows."""
     b, s, nimg = shape
-    print(f"splice {shape} padding_idx={padding_idx}", flush=True)
-    ids, emb, vis = make(b, s, 256 if s < 4096 else 151936, 128 if s < 4096 else 1536, nimg, padding_idx=padding_idx)
-    g = torch.randn(b, s, emb.weight.shape[1], generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(DEV)
+    print(f"splice {shape} padding_idx={padding_idx} dtype={dtype}", flush=True)
+    big = s >= 4096
+    vocab, hidden = (151936, 1536) if big else (256, 128)
+    ids, emb, vis = make(b, s, vocab, hidden, nimg, padding_idx=padding_idx, dtype=dtype)
+    g = torch.randn(b, s, hidden, generator=torch.Generator().manual_seed(1)).to(dtype).to(DEV)
     v1 = vis.clone().requires_grad_()
     w1 = emb.weight.detach().clone().requires_grad_()
-    out = S.splice_vision_tokens(ids, w1, v1, IMG, padding_idx)
+    out = S.splice_vision_tokens(ids, w1, v1, IMG, padding_idx, validate="sync")
     out.backward(g)
     emb.zero_grad(set_to_none=True)
     v2 = vis.clone().requires_grad_()
     ref = reference(ids, emb, v2)
     ref.backward(g)
     torch.cuda.synchronize()
-    assert torch.equal(bits(out), bits(ref))
-    assert torch.equal(bits(v1.grad), bits(v2.grad))
-    assert torch.equal(bits(w1.grad), bits(emb.weight.grad))
-    if s <= 300:
+    assert out.dtype == dtype
+    assert torch.equal(out, ref)
+    assert torch.equal(v1.grad, v2.grad)
+    # the table's gradient: one rounding of the exact per-id sum (fp32 accumulation of at most a few thousand
+    # rows stays far inside half a bf16 ulp; for fp32 tables the bound is the fp32 sum's own error)
+    exact = torch.from_numpy(table_grad_oracle(g.reshape(-1, hidden), ids.reshape(-1), vocab, padding_idx))
+    got = w1.grad.double().cpu()
+    if dtype == torch.bfloat16:
+        assert torch.equal(w1.grad.cpu(), exact.to(torch.bfloat16)) or \
+            bool(((got - exact).abs() <= 2.0**-8 * exact.abs() + 1e-30).all())
+    else:
+        assert bool(((got - exact).abs() <= 1e-5 * exact.abs().clamp_min(1.0)).all())
+    again = S.embedding_bwd(g.reshape(-1, hidden).contiguous(), ids.reshape(-1), vocab, (IMG, padding_idx))
+    assert torch.equal(again, w1.grad)  # deterministic
+    same_as_torch = torch.equal(w1.grad, emb.weight.grad)
+    print(f"  table gradient bitwise torch's: {same_as_torch}", flush=True)
+    if b * s > 3072:
+        assert same_as_torch
+    if s <= 300 and dtype == torch.bfloat16:
         ow = osp.splice_fwd(ids.cpu().numpy(), emb.weight.float().detach().cpu().numpy(),
                             vis.float().cpu().numpy(), IMG)
         assert np.array_equal(out.float().detach().cpu().numpy(), ow)
@@ -80,11 +116,34 @@ def test_forward_backward_bitwise(shape, padding_idx):
 def test_count_mismatch_and_bad_ids():
     ids, emb, vis = make(2, 50, 256, 64, 10)
     with pytest.raises(ValueError, match="Shape Mismatch"):
-        S.splice_vision_tokens(ids, emb.weight, vis[:9], IMG)
+        S.splice_vision_tokens(ids, emb.weight, vis[:9], IMG, validate="sync")
     bad = ids.clone()
     bad[0, 3] = 300
     with pytest.raises(IndexError):
-        S.splice_vision_tokens(bad, emb.weight, vis, IMG)
+        S.splice_vision_tokens(bad, emb.weight, vis, IMG, validate="sync")
+
+
+def test_lazy_checks_raise_later_and_never_read_garbage():
+    """The default validation: the call returns at once; the error comes at the
+    next call or check_pending_splices().  Meanwhile a backward through a call
+    with fewer placeholders than vision rows gathers zero rows for the missing
+    ones (image_pos holds -1 there), never memory past the gradient."""
+    S.check_pending_splices(block=True)
+    ids, emb, vis = make(2, 50, 256, 64, 10)
+    v = torch.cat([vis, vis[:3]]).requires_grad_()  # 13 vision rows, 10 placeholders
+    out = S.splice_vision_tokens(ids, emb.weight, v, IMG)
+    out.float().sum().backward()
+    torch.cuda.synchronize()
+    assert bool((v.grad[10:] == 0).all()) and bool((v.grad[:10] == 1).all())
+    with pytest.raises(ValueError, match="Shape Mismatch"):
+        S.check_pending_splices(block=True)
+    S.check_pending_splices(block=True)  # reported once
+    bad = ids.clone()
+    bad[1, 7] = -4
+    S.splice_vision_tokens(bad, emb.weight, vis, IMG)
+    with pytest.raises(IndexError):
+        S.splice_vision_tokens(ids, emb.weight, vis, IMG)  # raised at the next call
+    S.check_pending_splices(block=True)
 
 
 # ----------------------------------------------------------------- end to end
@@ -147,7 +206,7 @@ def grads(model):
     return {n: p.grad.detach().clone() for n, p in model.named_parameters() if p.grad is not None}
 
 
-def test_tiny_vlm_splice_only_bitwise():
+def test_tiny_vlm_splice_only():
     print("tiny VLM, splice only", flush=True)
     torch.manual_seed(0)
     model = TinyVLM().to(DEV).to(torch.bfloat16)
@@ -161,8 +220,16 @@ def test_tiny_vlm_splice_only_bitwise():
     out.loss.backward()
     g = grads(model)
     assert torch.equal(bits(out.logits), bits(out_ref.logits))
+    table = "text_model.model.embed_tokens.weight"
     for n in g_ref:
-        assert torch.equal(bits(g[n]), bits(g_ref[n])), n
+        if n == table:
+            # 120 tokens: torch's short-batch embedding backward rounds its running sum to bf16 per batch of 64
+            # tokens, the kernel once per id (exactly torch's sorted path, checked bitwise above), so where an
+            # id's rows nearly cancel the two differ by the intermediate roundings
+            r = float((g[n].double() - g_ref[n].double()).norm() / g_ref[n].double().norm())
+            assert r <= 1e-2, (n, r)
+        else:
+            assert torch.equal(bits(g[n]), bits(g_ref[n])), n
 
 
 def test_tiny_vlm_all_fused_vs_fp32():

@@ -121,3 +121,64 @@ def test_span_masked_labels_fraction_and_range():
     valid = lab[lab != -100]
     assert valid.min() >= 0 and valid.max() < 151936
     assert math.isclose(workloads.CONFIG4.flops(), 6.0 * 16384 * 1536 * 151936)
+
+
+def test_plan_describes_only_its_own_offsets():
+    """The host check behind an explicit ``plan=``: a plan accepts its own
+    offset copies, the unchanged tensors it was built from and equal values,
+    and refuses other offsets with the same totals and sequence count, or its
+    source tensor after an in-place change (CPU tensors stand in for the
+    device copies; the comparison is the same)."""
+    import weakref
+
+    src = torch.tensor([0, 100, 400, 600], dtype=torch.int32)
+    own = src.clone()
+    plan = attention.AttnPlan(None, 3, 600, 600, 12, 2, True, own, own,
+                              ((weakref.ref(src), src._version), (weakref.ref(src), src._version)))
+    assert plan.describes(own, own)
+    assert plan.describes(src, src)
+    assert plan.describes(src.clone(), torch.tensor([0, 100, 400, 600], dtype=torch.int64))
+    assert not plan.describes(torch.tensor([0, 300, 400, 600], dtype=torch.int32), own)
+    assert not plan.describes(own, torch.tensor([0, 600], dtype=torch.int32))
+    src[1] = 300
+    assert not plan.describes(src, src)
+    src[1] = 100  # same values again (a newer version): compared, and accepted
+    assert plan.describes(src, src)
+
+
+def test_fused_ce_patches_the_model_inside_a_peft_wrapper():
+    """Stage 2 with LoRA wraps the text model (siq_vl/model/modeling.py:388);
+    PEFT's wrapper forwards to the wrapped model's ``forward`` attribute, which
+    is what gets patched.  peft is not installed here: a stand-in with PEFT's
+    ``get_base_model()`` and forwarding shape plays the wrapper."""
+    transformers = pytest.importorskip("transformers")
+    from siq_vl_amd.text_model import enable_fused_cross_entropy, fused_causal_lm_forward
+
+    cfg = transformers.Qwen2Config(vocab_size=64, hidden_size=32, intermediate_size=64, num_hidden_layers=1,
+                                   num_attention_heads=2, num_key_value_heads=1, use_cache=False)
+    inner = transformers.Qwen2ForCausalLM(cfg)
+
+    class Wrapper(torch.nn.Module):
+        def __init__(self, m):
+            super().__init__()
+            self.base_model = torch.nn.Module()
+            self.base_model.model = m
+
+        def get_base_model(self):
+            return self.base_model.model
+
+        def forward(self, *args, **kwargs):
+            return self.base_model.model.forward(*args, **kwargs)
+
+    class VLM(torch.nn.Module):
+        def __init__(self, m):
+            super().__init__()
+            self.text_model = Wrapper(m)
+
+    vlm = VLM(inner)
+    patched = enable_fused_cross_entropy(vlm, chunk_tokens=256)
+    assert patched is inner
+    assert inner.forward.__func__ is fused_causal_lm_forward
+    # no labels: the logits path, reached through the wrapper
+    out = vlm.text_model(input_ids=torch.randint(0, 64, (1, 5)))
+    assert out.logits.shape == (1, 5, 64)
