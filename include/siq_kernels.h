@@ -51,6 +51,10 @@ enum siq_status {
   SIQ_ERR_LAUNCH = -5            /* the HIP runtime rejected a launch */
 };
 
+/* Element types of the entry points that take more than one. */
+#define SIQ_DTYPE_BF16 0
+#define SIQ_DTYPE_FP32 1
+
 /* Version of this ABI (SIQ_ABI_VERSION of the library that was built). */
 int siq_abi_version(void);
 
@@ -278,6 +282,27 @@ int siq_rope_fwd(const void* q, const void* k, const void* cos, const void* sin,
 int siq_rope_bwd(const void* dq_embed, const void* dk_embed, const void* cos, const void* sin, void* dq, void* dk,
                  int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides, void* stream);
 
+/* The same two passes with the dtype of cos / sin chosen (cs_dtype:
+ * SIQ_DTYPE_BF16 = siq_rope_fwd / _bwd, or SIQ_DTYPE_FP32).  fp32 cos / sin
+ * are what transformers' rotary embedding hands over under bf16 autocast
+ * over fp32 master weights (the reference's bf16=True training,
+ * scripts/train.py:712): there q and k are bf16 (autocast Linear outputs) and
+ * torch promotes q * cos + rotate_half(q) * sin to fp32, which the attention
+ * then casts to bf16.  siq_rope_fwd_ex writes that bf16 cast directly:
+ * q_embed = rb(fl(fl(q1 c1) - fl(q2 s1)), ...) with fp32 products and sum and
+ * one rounding to bf16, bitwise the reference's q_embed.to(bf16).
+ * siq_rope_bwd_ex is the reference's autograd of those ops on the bf16
+ * gradient of that cast: dq = rb(rb(fl(g1 c1)) + rb(fl(g2 s2))), ... .  With
+ * fp32 cos / sin their strides are multiples of 4 elements (16 bytes); the
+ * other tensors are as for siq_rope_fwd. */
+int siq_rope_fwd_ex(const void* q, const void* k, const void* cos, const void* sin, void* q_embed, void* k_embed,
+                    int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides,
+                    int cs_dtype, void* stream);
+
+int siq_rope_bwd_ex(const void* dq_embed, const void* dk_embed, const void* cos, const void* sin, void* dq, void* dk,
+                    int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides,
+                    int cs_dtype, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Pixel-shuffle projector (the vision-to-text bridge).
  *
@@ -355,9 +380,6 @@ int siq_gather_rows(const void* src, const int32_t* rows, int64_t n, int64_t hid
  * (SIQ_DTYPE_FP32, the reference's fp32 master weights); hidden % 8 == 0.
  * Workspace: siq_embedding_bwd_workspace_bytes(n_tokens, vocab).
  * ------------------------------------------------------------------------- */
-#define SIQ_DTYPE_BF16 0
-#define SIQ_DTYPE_FP32 1
-
 size_t siq_embedding_bwd_workspace_bytes(int64_t n_tokens, int64_t vocab);
 
 int siq_embedding_bwd(const void* grad, const int64_t* input_ids, int64_t n_tokens, int64_t vocab, int64_t hidden,

@@ -113,6 +113,16 @@ _PROTOS = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32, _i32, _i32,
          ctypes.POINTER(_i64), _c_void_p],
     ),
+    "siq_rope_fwd_ex": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32, _i32, _i32,
+         ctypes.POINTER(_i64), _i32, _c_void_p],
+    ),
+    "siq_rope_bwd_ex": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32, _i32, _i32,
+         ctypes.POINTER(_i64), _i32, _c_void_p],
+    ),
 }
 
 EXPORTED = tuple(_PROTOS)

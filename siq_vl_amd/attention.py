@@ -448,6 +448,43 @@ class _VarlenRopeAttnFn(torch.autograd.Function):
         return dq, dk, dv, None, None, None, None, None, None, None, None
 
 
+class _VarlenRopeF32Attn(torch.autograd.Function):
+    """The same pair with fp32 cos / sin rows (bf16 autocast over fp32 master
+    weights): one RoPE pass writes the bf16 q_embed / k_embed that the
+    reference's promoted fp32 rotation gives after the attention's cast
+    (``siq_rope_fwd_ex``), the attention runs on them, and one RoPE pass takes
+    the attention's dq_embed / dk_embed back through the rotation
+    (``siq_rope_bwd_ex``), as the reference's autograd does through the cast
+    and the promoted ops.  Bitwise the unfused path under autocast."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cos, sin, cu_q, cu_k, max_q, max_k, scale, causal):
+        from . import rope as _rope
+
+        cos, sin = cos.contiguous(), sin.contiguous()
+        qe, ke = _rope.rope_fwd(q[None], k[None], cos[None], sin[None])
+        qe, ke = qe[0], ke[0]
+        v = _ensure_token_major(v)
+        plan = cached_attn_plan(cu_q, cu_k, qe.shape[0], ke.shape[0], qe.shape[1], ke.shape[1], causal, qe.device)
+        out, lse = varlen_attn_fwd(qe, ke, v, cu_q, cu_k, max_q, max_k, scale, causal, plan=plan)
+        ctx.save_for_backward(qe, ke, v, out, lse, cos, sin)
+        ctx.plan = plan
+        ctx.args = (max_q, max_k, scale, causal)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        from . import rope as _rope
+
+        qe, ke, v, out, lse, cos, sin = ctx.saved_tensors
+        max_q, max_k, scale, causal = ctx.args
+        plan = ctx.plan
+        dqe, dke, dv = varlen_attn_bwd(_ensure_token_major(dout), qe, ke, v, out, lse, plan.cu_q, plan.cu_k, max_q,
+                                       max_k, scale, causal, plan=plan)
+        dq, dk = _rope.rope_bwd(dqe[None], dke[None], cos[None], sin[None])
+        return dq[0], dk[0], dv, None, None, None, None, None, None, None, None
+
+
 def flash_attn_varlen_rope_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
                                 sin: torch.Tensor, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
                                 max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float | None = None,
@@ -455,16 +492,19 @@ def flash_attn_varlen_rope_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tenso
     """``flash_attn_varlen_func(*apply_rotary_pos_emb(q, k, cos, sin), v)`` as
     one op: ``q [total, hq, d]`` and ``k [total, hkv, d]`` BEFORE rotation
     (self-attention: q and k rows are the same tokens), ``cos`` / ``sin
-    [total, d]`` the rows of each packed token.  Output and gradients are
-    bitwise those of the two separate ops."""
+    [total, d]`` the rows of each packed token, bf16 or fp32 (the latter under
+    bf16 autocast over fp32 master weights, where the reference rotates in
+    fp32 and the attention casts the result to bf16).  Output and gradients
+    are bitwise those of the two separate ops."""
     if cos.requires_grad or sin.requires_grad:
         raise ValueError("gradients with respect to cos / sin are not supported")
     if q.shape[0] != k.shape[0]:
         raise ValueError("the fused rotary attention needs q and k rows of the same tokens")
     if softmax_scale is None:
         softmax_scale = q.shape[-1] ** -0.5
-    return _VarlenRopeAttnFn.apply(q, k, v, cos, sin, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
-                                   int(max_seqlen_k), float(softmax_scale), bool(causal))
+    fn = _VarlenRopeF32Attn if cos.dtype == torch.float32 else _VarlenRopeAttnFn
+    return fn.apply(q, k, v, cos, sin, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), int(max_seqlen_k),
+                    float(softmax_scale), bool(causal))
 
 
 def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
@@ -633,12 +673,26 @@ def siq_varlen_attention_forward(module: torch.nn.Module, query: torch.Tensor, k
     d = query.shape[-1]
     if scaling is None:
         scaling = d**-0.5
-    target = query.dtype if query.dtype == torch.bfloat16 else torch.bfloat16
+    target = torch.bfloat16
     q = query.transpose(1, 2).to(target)
     k = key.transpose(1, 2).to(target)
     v = value.transpose(1, 2).to(target)
     out = _attend_packed(q, k, v, attention_mask, is_causal, scaling, kwargs)
-    return out.to(query.dtype).contiguous(), None
+    return out.to(_output_dtype(query)).contiguous(), None
+
+
+def _output_dtype(query: torch.Tensor) -> torch.dtype:
+    """The dtype the stock backends hand back: under bf16 autocast an fp32
+    query (the RoPE's output over fp32 master weights) gives bf16, as
+    ``F.scaled_dot_product_attention`` (an autocast lower-precision op) and
+    flash-attention's ``get_target_dtype`` (transformers
+    integrations/flash_attention.py:12-23) do, so no fp32 copy of the output
+    is made only to be cast back by ``o_proj``; otherwise the query's dtype."""
+    dev = query.device.type
+    if query.dtype == torch.float32 and torch.is_autocast_enabled(dev) and \
+            torch.get_autocast_dtype(dev) == torch.bfloat16:
+        return torch.bfloat16
+    return query.dtype
 
 
 def register(name: str = ATTN_IMPLEMENTATION) -> str:

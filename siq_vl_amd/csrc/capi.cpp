@@ -532,7 +532,8 @@ namespace {
 // q rows and k rows.  strides: x0 (b, s, h), x1 (b, s, h), cos (b, s),
 // sin (b, s), y0 (b, s, h), y1 (b, s, h).
 int rope_call(bool backward, const void* x0, const void* x1, const void* cosp, const void* sinp, void* y0, void* y1,
-              int64_t batch, int64_t seqlen, int hq, int hkv, int d, const int64_t* st, void* stream) {
+              int64_t batch, int64_t seqlen, int hq, int hkv, int d, const int64_t* st, void* stream,
+              int cs_dtype = SIQ_DTYPE_BF16) {
   const char* nm[6] = {backward ? "dq_embed" : "q", backward ? "dk_embed" : "k", "cos", "sin",
                        backward ? "dq" : "q_embed", backward ? "dk" : "k_embed"};
   if (batch < 0 || seqlen < 0) return fail(SIQ_ERR_INVALID_ARGUMENT, "batch and seqlen must be >= 0");
@@ -542,6 +543,8 @@ int rope_call(bool backward, const void* x0, const void* x1, const void* cosp, c
   if (d < 16 || d > 512 || d % 16 != 0)
     return fail(SIQ_ERR_UNSUPPORTED, "head_dim %d unsupported (a multiple of 16 in [16, 512])", d);
   if (st == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "strides must not be NULL");
+  if (cs_dtype != SIQ_DTYPE_BF16 && cs_dtype != SIQ_DTYPE_FP32)
+    return fail(SIQ_ERR_INVALID_ARGUMENT, "cos / sin dtype must be SIQ_DTYPE_BF16 or SIQ_DTYPE_FP32");
   if (batch * seqlen == 0) return ok();
   if (batch * seqlen >= (int64_t(1) << 32) || batch >= (int64_t(1) << 31) || seqlen >= (int64_t(1) << 31))
     return fail(SIQ_ERR_INVALID_ARGUMENT, "batch * seqlen must be < 2^32");
@@ -551,11 +554,13 @@ int rope_call(bool backward, const void* x0, const void* x1, const void* cosp, c
     if (hq == 0 && (t == 0 || t == 4)) continue;  // k-only pass: q and its output are not touched
     if (ptr[t] == nullptr) return fail(SIQ_ERR_INVALID_ARGUMENT, "%s must not be NULL", nm[t]);
     if (!aligned16(ptr[t])) return fail(SIQ_ERR_ALIGNMENT, "%s is not 16-byte aligned", nm[t]);
+    // 16-byte steps: 8 bf16 elements, or 4 fp32 elements for fp32 cos / sin
+    const int64_t step = (cs_dtype == SIQ_DTYPE_FP32 && (t == 2 || t == 3)) ? 4 : 8;
     for (int j = 0; j < count[t]; ++j) {
       const int64_t v = st[first[t] + j];
-      if (v < 0 || (v & 7))
-        return fail(SIQ_ERR_ALIGNMENT, "%s stride %d (%lld) must be a non-negative multiple of 8 elements", nm[t], j,
-                    (long long)v);
+      if (v < 0 || v % step)
+        return fail(SIQ_ERR_ALIGNMENT, "%s stride %d (%lld) must be a non-negative multiple of %lld elements", nm[t],
+                    j, (long long)v, (long long)step);
     }
   }
   auto ten = [&](int t) {
@@ -578,6 +583,7 @@ int rope_call(bool backward, const void* x0, const void* x1, const void* cosp, c
   a.hq = hq;
   a.hkv = hkv;
   a.d = d;
+  a.cs_f32 = cs_dtype == SIQ_DTYPE_FP32 ? 1 : 0;
   const hipError_t e = siq::launch_rope(a, backward, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(SIQ_ERR_LAUNCH, "rope launch failed: %s", hipGetErrorString(e));
   return ok();
@@ -595,6 +601,20 @@ int siq_rope_fwd(const void* q, const void* k, const void* cos, const void* sin,
 int siq_rope_bwd(const void* dq_embed, const void* dk_embed, const void* cos, const void* sin, void* dq, void* dk,
                  int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides, void* stream) {
   return rope_call(true, dq_embed, dk_embed, cos, sin, dq, dk, batch, seqlen, hq, hkv, head_dim, strides, stream);
+}
+
+int siq_rope_fwd_ex(const void* q, const void* k, const void* cos, const void* sin, void* q_embed, void* k_embed,
+                    int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides,
+                    int cs_dtype, void* stream) {
+  return rope_call(false, q, k, cos, sin, q_embed, k_embed, batch, seqlen, hq, hkv, head_dim, strides, stream,
+                   cs_dtype);
+}
+
+int siq_rope_bwd_ex(const void* dq_embed, const void* dk_embed, const void* cos, const void* sin, void* dq, void* dk,
+                    int64_t batch, int64_t seqlen, int hq, int hkv, int head_dim, const int64_t* strides,
+                    int cs_dtype, void* stream) {
+  return rope_call(true, dq_embed, dk_embed, cos, sin, dq, dk, batch, seqlen, hq, hkv, head_dim, strides, stream,
+                   cs_dtype);
 }
 
 }  // extern "C"

@@ -120,6 +120,42 @@ __device__ __forceinline__ void rope_bwd8(const bf16x8& g1, const bf16x8& g2, co
   }
 }
 
+// The same rotation with fp32 cos / sin rows (bf16 q / k under bf16 autocast
+// over fp32 master weights, where transformers' rotary embedding hands over
+// fp32 cos / sin): torch promotes every product and the sum to fp32, and the
+// attention's cast to bf16 rounds once at the end:
+//   o1 = rb(fl(fl(x1 c1) - fl(x2 s1))),  o2 = rb(fl(fl(x2 c2) + fl(x1 s2))),
+// with fl = fp32 rounding (no fused multiply-add: each product is made opaque
+// before the add).
+__device__ __forceinline__ float opq(float x) {
+  asm("" : "+v"(x));
+  return x;
+}
+__device__ __forceinline__ void rope_fwd8_f32(const bf16x8& x1, const bf16x8& x2, const float (&c1)[8],
+                                              const float (&c2)[8], const float (&s1)[8], const float (&s2)[8],
+                                              bf16x8& o1, bf16x8& o2) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float u = (float)x1[k], v = (float)x2[k];
+    o1[k] = (bf16)(opq(u * c1[k]) - opq(v * s1[k]));
+    o2[k] = (bf16)(opq(v * c2[k]) + opq(u * s2[k]));
+  }
+}
+
+// Its autograd backward: each product's gradient is formed in fp32 and cast
+// to the bf16 input's dtype, and the two contributions to x are added in bf16:
+//   dx1 = rb(rb(fl(g1 c1)) + rb(fl(g2 s2))),  dx2 = rb(rb(fl(g2 c2)) - rb(fl(g1 s1))).
+__device__ __forceinline__ void rope_bwd8_f32(const bf16x8& g1, const bf16x8& g2, const float (&c1)[8],
+                                              const float (&c2)[8], const float (&s1)[8], const float (&s2)[8],
+                                              bf16x8& o1, bf16x8& o2) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float u = (float)g1[k], v = (float)g2[k];
+    o1[k] = (bf16)(rbf(u * c1[k]) + rbf(v * s2[k]));
+    o2[k] = (bf16)(rbf(v * c2[k]) - rbf(u * s1[k]));
+  }
+}
+
 __device__ __forceinline__ float wave_max_xor32(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 __device__ __forceinline__ float wave_sum_xor32(float x) { return x + __shfl_xor(x, 32); }
 

@@ -17,9 +17,10 @@ struct RopeTensor {
 struct RopeArgs {
   RopeTensor x[2];  // inputs: q, k (forward) or dq_embed, dk_embed (backward)
   RopeTensor y[2];  // outputs: q_embed, k_embed (forward) or dq, dk (backward)
-  RopeTensor cos, sin;
+  RopeTensor cos, sin;  // bf16, or fp32 when cs_f32 (p then points at floats; strides in floats)
   int64_t batch, seqlen;
   int hq, hkv, d;
+  int cs_f32;
 };
 
 // Needs d a multiple of 16 in [16, 512] and batch * seqlen < 2^32.

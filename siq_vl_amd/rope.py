@@ -55,23 +55,34 @@ def _prep(t: torch.Tensor, rank: int) -> torch.Tensor:
     return t if _usable(t, rank) else t.contiguous()
 
 
+_CS_DTYPE = {torch.bfloat16: 0, torch.float32: 1}  # SIQ_DTYPE_BF16 / SIQ_DTYPE_FP32
+
+
 def _launch(fn_name: str, x0, x1, cos, sin, y0, y1) -> None:
     b, s, hq, d = x0.shape
     hkv = x1.shape[2]
     strides = [*x0.stride()[:3], *x1.stride()[:3], *cos.stride()[:2], *sin.stride()[:2], *y0.stride()[:3],
                *y1.stride()[:3]]
     stream = torch.cuda.current_stream(x0.device).cuda_stream
-    rc = getattr(_lib.lib(), fn_name)(x0.data_ptr(), x1.data_ptr(), cos.data_ptr(), sin.data_ptr(), y0.data_ptr(),
-                                      y1.data_ptr(), b, s, hq, hkv, d, _lib.int64_array(strides), stream)
+    rc = getattr(_lib.lib(), fn_name + "_ex")(x0.data_ptr(), x1.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                              y0.data_ptr(), y1.data_ptr(), b, s, hq, hkv, d,
+                                              _lib.int64_array(strides), _CS_DTYPE[cos.dtype], stream)
     _lib.check(rc, fn_name)
 
 
 def _check(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> None:
+    """q / k bf16; cos / sin bf16, or both fp32 (bf16 autocast over fp32
+    master weights: the outputs are then the bf16 rounding of torch's
+    promoted fp32 result)."""
     for name, t in (("q", q), ("k", k), ("cos", cos), ("sin", sin)):
-        if t.dtype != torch.bfloat16:
-            raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+        ok = t.dtype == torch.bfloat16 or (name in ("cos", "sin") and t.dtype == torch.float32)
+        if not ok:
+            raise ValueError(f"{name} must be bfloat16{' or float32' if name in ('cos', 'sin') else ''}, "
+                             f"got {t.dtype}")
         if t.device.type != "cuda":
             raise ValueError(f"{name} must live on the GPU, got {t.device}")
+    if cos.dtype != sin.dtype:
+        raise ValueError(f"cos and sin must have one dtype, got {cos.dtype} and {sin.dtype}")
     b, s, _, d = q.shape
     if k.shape[0] != b or k.shape[1] != s or k.shape[3] != d:
         raise ValueError(f"k {tuple(k.shape)} does not match q {tuple(q.shape)} in batch / seqlen / head_dim")
@@ -85,7 +96,9 @@ def _expand_cs(t: torch.Tensor, b: int) -> torch.Tensor:
 
 
 def rope_fwd(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
-    """Raw forward on ``[B, S, H, D]`` views; returns ``(q_embed, k_embed)`` laid out like q and k."""
+    """Raw forward on ``[B, S, H, D]`` views; returns ``(q_embed, k_embed)``
+    (bf16) laid out like q and k.  With fp32 cos / sin: the bf16 rounding of
+    the fp32 result torch's promotion gives (``siq_rope_fwd_ex``)."""
     _check(q, k, cos, sin)
     q, k = _prep(q, 4), _prep(k, 4)
     cos, sin = _prep(_expand_cs(cos, q.shape[0]), 3), _prep(_expand_cs(sin, q.shape[0]), 3)
@@ -162,8 +175,9 @@ def _launch_k(fn_name: str, x1, cos, sin, y1) -> None:
     b, s, hkv, d = x1.shape
     strides = [0, 0, 0, *x1.stride()[:3], *cos.stride()[:2], *sin.stride()[:2], 0, 0, 0, *y1.stride()[:3]]
     stream = torch.cuda.current_stream(x1.device).cuda_stream
-    rc = getattr(_lib.lib(), fn_name)(None, x1.data_ptr(), cos.data_ptr(), sin.data_ptr(), None, y1.data_ptr(), b, s,
-                                      0, hkv, d, _lib.int64_array(strides), stream)
+    rc = getattr(_lib.lib(), fn_name + "_ex")(None, x1.data_ptr(), cos.data_ptr(), sin.data_ptr(), None,
+                                              y1.data_ptr(), b, s, 0, hkv, d, _lib.int64_array(strides),
+                                              _CS_DTYPE[cos.dtype], stream)
     _lib.check(rc, fn_name)
 
 
@@ -212,15 +226,23 @@ def fused_qwen2_attention_forward(self, hidden_states: torch.Tensor, position_em
     attention as one op (``flash_attn_varlen_rope_func``): the rotation's
     backward of q runs inside the attention backward's dQ kernel.  Same
     signature and return; bitwise the outputs and gradients of the unfused
-    path (``enable_fused_rope`` + ``siq_varlen``).  Calls it cannot serve (a
-    KV cache, another attention backend, non-bf16 or CPU tensors) take the
-    stock forward."""
+    path (``enable_fused_rope`` + ``siq_varlen``), for a bf16 model and under
+    bf16 autocast over fp32 master weights (fp32 cos / sin: the rotation in
+    fp32, rounded once to bf16 as the attention's cast rounds the reference's
+    fp32 q_embed / k_embed).  Calls it cannot serve (a KV cache, another
+    attention backend, fp32 projections or CPU tensors) take the stock
+    forward."""
     from .attention import ATTN_IMPLEMENTATION, _attend_packed
 
     cos, sin = position_embeddings
+    # bf16 projections: a bf16 model, or bf16 autocast over fp32 master weights (the reference's bf16=True
+    # training, scripts/train.py:712), where the rotary embedding hands over fp32 cos / sin
+    bf16_proj = hidden_states.dtype == torch.bfloat16 or (
+        hidden_states.is_cuda and torch.is_autocast_enabled("cuda")
+        and torch.get_autocast_dtype("cuda") == torch.bfloat16)
     usable = (past_key_values is None and getattr(self.config, "_attn_implementation", None) == ATTN_IMPLEMENTATION
-              and hidden_states.is_cuda and hidden_states.dtype == torch.bfloat16
-              and cos.dtype == torch.bfloat16 and sin.dtype == torch.bfloat16
+              and hidden_states.is_cuda and bf16_proj and cos.dtype == sin.dtype
+              and cos.dtype in (torch.bfloat16, torch.float32)
               and getattr(self, "sliding_window", None) is None and self.head_dim in (64, 128))
     if not usable:
         return type(self).forward(self, hidden_states, position_embeddings, attention_mask,
@@ -233,6 +255,8 @@ def fused_qwen2_attention_forward(self, hidden_states: torch.Tensor, position_em
     q = self.q_proj(hidden_states).view(hidden_shape)  # [B, S, Hq, D]: the token-major layout the kernels read
     k = self.k_proj(hidden_states).view(hidden_shape)
     v = self.v_proj(hidden_states).view(hidden_shape)
+    if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
+        raise ValueError("the fused rotary attention expects bf16 projections")
     out = _attend_packed(q, k, v, attention_mask, bool(self.is_causal), self.scaling, kwargs, rope=(cos, sin))
     attn_output = out.reshape(*input_shape, -1).contiguous()
     return self.o_proj(attn_output), None

@@ -336,3 +336,29 @@ def test_rope_empty_is_a_no_op(lib):
     # nothing to rotate: returns before touching the device (pointers are never read)
     assert _rope(lib, seqlen=0) == _lib.SIQ_OK
     assert _rope(lib, False, batch=0) == _lib.SIQ_OK
+
+
+def test_embedding_bwd_validation(lib):
+    """siq_embedding_bwd rejects bad arguments before any launch (CPU: no
+    device pointer is ever dereferenced)."""
+    ws_need = lib.siq_embedding_bwd_workspace_bytes(100, 1000)
+    assert ws_need > 100 * 8 and lib.siq_embedding_bwd_workspace_bytes(-1, 1000) == 0
+    assert lib.siq_embedding_bwd_workspace_bytes(0, 1000) > 0
+    base = dict(grad=FAKE, ids=FAKE, n=100, vocab=1000, hidden=64, dtype=0, s0=5, s1=-1, dw=FAKE, ws=FAKE,
+                ws_bytes=ws_need)
+
+    def call(**kw):
+        a = dict(base, **kw)
+        return lib.siq_embedding_bwd(a["grad"], a["ids"], a["n"], a["vocab"], a["hidden"], a["dtype"], a["s0"],
+                                     a["s1"], a["dw"], a["ws"], a["ws_bytes"], None)
+
+    assert call(n=-1) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    assert call(vocab=0) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    assert call(hidden=60) == _lib.SIQ_ERR_UNSUPPORTED
+    assert call(dtype=2) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    assert call(dw=None) == _lib.SIQ_ERR_ALIGNMENT
+    assert call(dw=FAKE + 8) == _lib.SIQ_ERR_ALIGNMENT
+    assert call(grad=None) == _lib.SIQ_ERR_INVALID_ARGUMENT
+    assert call(ws_bytes=ws_need - 1) == _lib.SIQ_ERR_WORKSPACE
+    assert call(ws=None) == _lib.SIQ_ERR_WORKSPACE
+    assert "workspace" in lib.siq_last_error().decode()

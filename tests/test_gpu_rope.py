@@ -210,3 +210,40 @@ def test_in_place_through_the_abi():
     bk = R._bshd(k, 1).contiguous()
     R._launch("siq_rope_fwd", bq, bk, cos, sin, bq, bk)  # outputs are the inputs
     assert same(bq, R._bshd(rq, 1)) and same(bk, R._bshd(rk, 1))
+
+
+def fp32_cos_sin(b, s, d, theta=1000000.0):
+    """cos / sin as Qwen2RotaryEmbedding returns them for fp32 hidden states
+    (bf16 autocast over fp32 master weights): fp32, not rounded to bf16."""
+    pos = torch.arange(s, dtype=torch.float32).repeat(b, 1)
+    inv = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    emb = torch.cat([pos[..., None] * inv, pos[..., None] * inv], dim=-1)
+    return emb.cos().to(DEV), emb.sin().to(DEV)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_fp32_cos_sin_is_the_promoted_rotation_rounded_once(d):
+    """bf16 q / k with fp32 cos / sin (the reference's bf16=True training):
+    torch promotes q * cos + rotate_half(q) * sin to fp32 and the attention
+    casts the result to bf16.  siq_rope_fwd_ex writes that bf16 value, bitwise
+    (checked against torch on the GPU and against fp32 torch on the CPU), and
+    siq_rope_bwd_ex is the autograd of the promoted ops and the cast, bitwise."""
+    b, s, hq, hkv = 2, 45, 6, 2
+    print(f"rope fp32 cos/sin d={d}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    q, k = projected(b, s, hq, d, g), projected(b, s, hkv, d, g)
+    cos, sin = fp32_cos_sin(b, s, d)
+    qe, ke = R.rope_fwd(q.transpose(1, 2), k.transpose(1, 2), cos, sin)
+    rq, rk = torch_rope(q, k, cos, sin)
+    assert rq.dtype == torch.float32
+    assert same(qe.transpose(1, 2), rq.to(torch.bfloat16)) and same(ke.transpose(1, 2), rk.to(torch.bfloat16))
+    cq, ck = torch_rope(q.cpu(), k.cpu(), cos.cpu(), sin.cpu())
+    assert same(qe.transpose(1, 2), cq.to(torch.bfloat16)) and same(ke.transpose(1, 2), ck.to(torch.bfloat16))
+    # backward through the promoted ops and the cast
+    gq = torch.randn(b, hq, s, d, generator=g).to(torch.bfloat16).to(DEV)
+    gk = torch.randn(b, hkv, s, d, generator=g).to(torch.bfloat16).to(DEV)
+    xq, xk = q.detach().clone().requires_grad_(), k.detach().clone().requires_grad_()
+    oq, ok = torch_rope(xq, xk, cos, sin)
+    torch.autograd.backward([oq.to(torch.bfloat16), ok.to(torch.bfloat16)], [gq, gk])
+    dq, dk = R.rope_bwd(gq.transpose(1, 2), gk.transpose(1, 2), cos, sin)
+    assert same(dq.transpose(1, 2), xq.grad) and same(dk.transpose(1, 2), xk.grad)

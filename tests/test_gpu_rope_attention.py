@@ -149,6 +149,43 @@ def test_dropin_qwen2_bitwise(route, head_dim):
             assert same(grads[n], ref_grads[n]), n
 
 
+@pytest.mark.parametrize("route", ["cu_seq_lens", "position_ids"])
+def test_dropin_qwen2_autocast_over_fp32_weights_bitwise(route):
+    """The reference's bf16=True training: fp32 master weights, bf16 autocast
+    (scripts/train.py:712), so the rotary embedding hands fp32 cos / sin to
+    bf16 q / k and the rotation runs in fp32.  With the rotation fused into
+    the attention (fp32 rotation rounded once to bf16, as the attention's cast
+    rounds it) the logits and every parameter gradient are bitwise those of
+    siq_varlen alone with the stock rotation."""
+    print(f"rope+attention drop-in under autocast route={route}", flush=True)
+    lengths = [37, 130, 1, 64, 90]
+    g = torch.Generator().manual_seed(3)
+    ids = [torch.randint(0, 512, (n,), generator=g) for n in lengths]
+    flat = torch.cat(ids)[None]
+    pos = torch.cat([torch.arange(n) for n in lengths])[None]
+    kwargs = {"input_ids": flat.to(DEV), "position_ids": pos.to(DEV)}
+    if route == "cu_seq_lens":
+        cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0).tolist()), dtype=torch.int32, device=DEV)
+        kwargs.update(cu_seq_lens_q=cu, cu_seq_lens_k=cu, max_length_q=max(lengths), max_length_k=max(lengths))
+    model = _qwen(128).float()
+
+    def run():
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            logits = model(**kwargs).logits
+        logits.float().square().mean().backward()
+        return logits.detach(), {n: p.grad.detach().clone() for n, p in model.named_parameters()}
+
+    ref_logits, ref_grads = run()
+    assert R.enable_fused_rope_attention(model) == 2
+    logits, grads = run()
+    assert logits.dtype == torch.bfloat16
+    assert same(logits, ref_logits)
+    for n in ref_grads:
+        if "embed_tokens" not in n:  # the embedding gradient is an atomic scatter-add
+            assert same(grads[n], ref_grads[n]), n
+
+
 def test_dropin_falls_back_where_it_cannot_fuse():
     # fp32 activations: the stock forward (with the stock rotation) runs unchanged
     model = _qwen(64).float()
