@@ -149,6 +149,25 @@ def timed_steps(parts, steps: int, warmup: int) -> dict:
     return res
 
 
+def host_ahead_ms(fn, steps: int, warmup: int) -> float:
+    """Median GPU time per call of ``fn`` with the host running ahead, as in a
+    training step: a spin kernel holds the stream while the calls are enqueued
+    behind it, so the events between calls time the GPU's work, not the
+    host's launch overhead."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = _events(steps + 1)
+    torch.cuda._sleep(100_000_000)
+    ev[0].record(stream)
+    for i in range(steps):
+        fn()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    return _median([ev[i].elapsed_time(ev[i + 1]) for i in range(steps)])
+
+
 GRAPH_STEPS_PER_REPLAY = 4
 
 
@@ -411,10 +430,35 @@ def bench_rope_attention(steps: int, warmup: int) -> dict:
         out, lse = A.varlen_attn_fwd(q, k, v, cu, cu, 0, 0, scale, True, plan=plan)
         A.varlen_attn_bwd(do, q, k, v, out, lse, cu, cu, 0, 0, scale, True, plan=plan)
 
+    # bf16 autocast over fp32 master weights (the reference's bf16=True training): fp32 cos / sin.  The stock
+    # path rotates in fp32 (torch's promoted ops and their autograd) and casts q_embed / k_embed to bf16 for
+    # the attention; the fused path writes the bf16 cast directly (siq_rope_fwd_ex / siq_rope_bwd_ex)
+    cos32, sin32 = emb.cos().to(dev), emb.sin().to(dev)
+    qg, kg = q.detach().clone().requires_grad_(), k.detach().clone().requires_grad_()
+
+    def rotate_half(x):
+        return torch.cat((-x[..., d // 2:], x[..., : d // 2]), dim=-1)
+
+    def autocast_stock():
+        qe = (qg * cos32[:, None]) + (rotate_half(qg) * sin32[:, None])
+        ke = (kg * cos32[:, None]) + (rotate_half(kg) * sin32[:, None])
+        out = A.flash_attn_varlen_func(qe.to(torch.bfloat16), ke.to(torch.bfloat16), v, cu, cu, 0, 0,
+                                       softmax_scale=scale, causal=True)
+        out.backward(do)
+
+    def autocast_fused():
+        out = A.flash_attn_varlen_rope_func(qg, kg, v, cos32, sin32, cu, cu, 0, 0, softmax_scale=scale,
+                                            causal=True)
+        out.backward(do)
+
     res = {}
     for name, fn in (("attention_only", attention_only), ("unfused", unfused), ("dropin", dropin),
                      ("fused_fwd", fused_fwd)):
         res[name + "_ms"] = graphed_ms(fn, 5, steps, warmup)
+    # autograd steps, timed with the host running ahead (the stock path's many small ops cost GPU time, not
+    # only launches); the attention's plan is cached on cu after the first call
+    res["autocast_stock_ms"] = host_ahead_ms(autocast_stock, steps, warmup)
+    res["autocast_fused_ms"] = host_ahead_ms(autocast_fused, steps, warmup)
     return res
 
 
@@ -522,26 +566,10 @@ def bench_splice(steps: int, warmup: int) -> dict:
         positions = (ids == img).nonzero(as_tuple=True)
         te[positions] = vis
 
-    def queued(fn):
-        """GPU time per call with the host running ahead (as in a training step): a spin kernel holds the
-        stream while the calls are enqueued behind it, so the events time the GPU, not the host."""
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        ev = _events(steps + 1)
-        torch.cuda._sleep(40_000_000)
-        ev[0].record(stream)
-        for i in range(steps):
-            fn()
-            ev[i + 1].record(stream)
-        torch.cuda.synchronize()
-        per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
-        return per[len(per) // 2]
-
     ref_ms = timed(ref_step, 1)
     op_ms = timed(lambda: SP.splice_vision_tokens(ids, weight, vis, img), 1)
     op_sync_ms = timed(lambda: SP.splice_vision_tokens(ids, weight, vis, img, validate="sync"), 1)
-    op_queued_ms = queued(lambda: SP.splice_vision_tokens(ids, weight, vis, img))
+    op_queued_ms = host_ahead_ms(lambda: SP.splice_vision_tokens(ids, weight, vis, img), steps, warmup)
     SP.check_pending_splices(block=True)
     # the embedding table's gradient (full fine-tune): the HIP per-id sum against torch's embedding backward
     gout = torch.randn(n, hidden, generator=g).to(torch.bfloat16).to(dev)
@@ -796,7 +824,8 @@ def main() -> int:
         print(f"[bench] config 2 with RoPE (graph-replayed): attention alone {ropeattn['attention_only_ms'] * 1e3:.1f} "
               f"us, unfused {ropeattn['unfused_ms'] * 1e3:.1f} us, drop-in (dq rotation in the dQ kernel) "
               f"{ropeattn['dropin_ms'] * 1e3:.1f} us, q also rotated in the forward {ropeattn['fused_fwd_ms'] * 1e3:.1f} "
-              f"us", file=sys.stderr, flush=True)
+              f"us; under autocast over fp32 weights: stock {ropeattn['autocast_stock_ms'] * 1e3:.1f} us, fused "
+              f"{ropeattn['autocast_fused_ms'] * 1e3:.1f} us", file=sys.stderr, flush=True)
     proj = None
     if not args.skip_projector:
         proj = bench_projector(leg_steps, args.warmup)
@@ -901,7 +930,15 @@ def main() -> int:
             "unfused_us": round(ropeattn["unfused_ms"] * 1e3, 2), "dropin_us": round(ropeattn["dropin_ms"] * 1e3, 2),
             "fused_fwd_us": round(ropeattn["fused_fwd_ms"] * 1e3, 2),
             "rope_round_trip_unfused_us": round((ropeattn["unfused_ms"] - ropeattn["attention_only_ms"]) * 1e3, 2),
-            "rope_cost_dropin_us": round((ropeattn["dropin_ms"] - ropeattn["attention_only_ms"]) * 1e3, 2)}
+            "rope_cost_dropin_us": round((ropeattn["dropin_ms"] - ropeattn["attention_only_ms"]) * 1e3, 2),
+            "autocast": {
+                "workload": "the same step under bf16 autocast over fp32 master weights (fp32 cos / sin): stock = "
+                            "torch's promoted fp32 rotation + casts to bf16 + attention + autograd; fused = "
+                            "flash_attn_varlen_rope_func (siq_rope_fwd_ex / _bwd_ex around the attention); "
+                            "bitwise the same gradients",
+                "timing": "eager autograd steps queued behind a spin kernel (GPU time per step)",
+                "stock_us": round(ropeattn["autocast_stock_ms"] * 1e3, 2),
+                "fused_us": round(ropeattn["autocast_fused_ms"] * 1e3, 2)}}
     if proj is not None:
         line["projector"] = {
             "workload": "pixel-shuffle projector fwd+bwd (dx, dweight): 16 tiles x 32x32 patches x 1024 -> r 2 -> "
