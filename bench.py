@@ -592,7 +592,13 @@ def bench_ce(steps: int, warmup: int, chunk: int | None) -> dict:
     def step():
         return C.flce_fwd_bwd(x["hidden"], x["weight"], x["labels"], chunk_tokens=chunk)
 
+    def step_dh():
+        # a frozen lm_head (the reference's stage 1, and stage 2's LoRA, which leaves lm_head out of its
+        # targets): loss and dHidden only, no dW GEMM
+        return C.flce_fwd_bwd(x["hidden"], x["weight"], x["labels"], need_dweight=False, chunk_tokens=chunk)
+
     r = timed_steps([("ce", step)], steps, warmup)
+    r_dh = timed_steps([("ce_dh", step_dh)], steps, warmup)
     ms = r["median_ms"]
     # tokens/s counts every row of the batch (the metric); the executed TFLOP/s counts the work the
     # kernels run: rows whose label is ignored are compacted out before the logits GEMM
@@ -604,6 +610,7 @@ def bench_ce(steps: int, warmup: int, chunk: int | None) -> dict:
         "tflops_all_rows": 6.0 * cfg.n * cfg.hdim * cfg.vocab / (ms * 1e-3) / 1e12,
         "tflops_executed": 6.0 * n_valid * cfg.hdim * cfg.vocab / (ms * 1e-3) / 1e12,
         "chunk": chunk, "workspace_bytes": ws,
+        "dh_only_ms": r_dh["median_ms"], "dh_only_workspace_bytes": C.flce_workspace_bytes(cfg.n, cfg.hdim, cfg.vocab, chunk, False),
         "e_bytes": 2 * chunk * cfg.vocab,
         "algorithmic_bytes": 2 * (2 * cfg.n * cfg.hdim + 2 * cfg.vocab * cfg.hdim) + 8 * cfg.n,
     }
@@ -810,7 +817,8 @@ def main() -> int:
         ce = bench_ce(leg_steps, args.warmup, args.ce_chunk)
         print(f"[bench] config 4 fused CE {ce['ms_per_step']:.3f} ms/step (median), {ce['tokens_per_s']:.3e} tokens/s, "
               f"{ce['tflops_all_rows']:.1f} TFLOP/s over all rows, {ce['tflops_executed']:.1f} executed "
-              f"(chunk {ce['chunk']} rows)", file=sys.stderr, flush=True)
+              f"(chunk {ce['chunk']} rows); dH only (frozen lm_head) {ce['dh_only_ms']:.3f} ms/step",
+              file=sys.stderr, flush=True)
     rope = None
     if not args.skip_rope:
         rope = bench_rope(leg_steps, args.warmup)
@@ -894,6 +902,7 @@ def main() -> int:
         line["attention_configs"]["5"]["cpu_baseline"] = cpu["attn_config5"]
     if ce is not None:
         traffic_ce = measured_traffic("ce_config4")
+        cfg4_n = W.CONFIG4.n
         line["ce"] = {"workload": "config 4: fused linear CE fwd+bwd, h [16384,1536], W [151936,1536], 30% span mask",
                       "tokens_per_s": round(ce["tokens_per_s"], 1), "ms_per_step": round(ce["ms_per_step"], 4),
                       "mean_ms_per_step": round(ce["mean_ms_per_step"], 4),
@@ -908,7 +917,15 @@ def main() -> int:
                                    "work": "6 * rows_with_label * hdim * vocab",
                                    "traffic": traffic_ce["bytes"], "traffic_source": traffic_ce,
                                    "algorithmic_bytes": ce["algorithmic_bytes"]},
-                      "cpu_baseline": cpu["ce"] if cpu else None}
+                      "cpu_baseline": cpu["ce"] if cpu else None,
+                      "dh_only": {"workload": "the same call with a frozen lm_head (dweight = NULL): loss and dHidden "
+                                              "only, as the reference trains in stage 1 and stage 2 with LoRA",
+                                  "ms_per_step": round(ce["dh_only_ms"], 4),
+                                  "tokens_per_s": round(cfg4_n / (ce["dh_only_ms"] * 1e-3), 1),
+                                  "tflops_executed": round(4.0 * ce["n_valid"] * W.CONFIG4.hdim * W.CONFIG4.vocab
+                                                           / (ce["dh_only_ms"] * 1e-3) / 1e12, 2),
+                                  "work": "4 * rows_with_label * hdim * vocab (logits and dH GEMMs)",
+                                  "workspace_bytes": ce["dh_only_workspace_bytes"]}}
     if rope is not None:
         line["rope"] = {"workload": "config-2 shape: RoPE of q [16384,12,128] and k [16384,2,128] (Qwen2 layout, "
                                     "packed position ids), forward and backward",

@@ -124,15 +124,24 @@ inline int64_t kv_item_cap(int64_t total_k, int batch) {
   return tile_cap(total_k, batch, kBwdBN) + 2 * kSplitTarget + 1;
 }
 
-// True when the plan was built for these arguments (read by one lane; the
-// caller returns on false).  A mismatch is recorded in the plan's status_use.
-__device__ __forceinline__ bool plan_matches(const AttnParams& p, bool causal, bool need_kv) {
-  const PlanHeader h = *p.plan;
-  const bool ok = h.magic == kPlanMagic && h.total_q == p.total_q && h.total_k == p.total_k &&
-                  h.batch == p.batch && h.n_rep == p.n_rep && h.hkv == p.hkv && h.causal == (causal ? 1 : 0) &&
-                  (!need_kv || h.has_kv);
+// The plan header, read whole.  A kernel issues this load before the load of
+// its work-list entry and waits for both together (one memory round trip at
+// the start of every workgroup instead of three dependent ones).
+__device__ __forceinline__ PlanHeader plan_header(const AttnParams& p) { return *p.plan; }
+
+// True when the plan was built for these arguments; the caller returns on
+// false.  Every field is compared (no short-circuit, so no field waits on
+// another's test).  A mismatch is recorded in the plan's status_use.
+__device__ __forceinline__ bool plan_header_ok(const PlanHeader& h, const AttnParams& p, bool causal, bool need_kv) {
+  const bool ok = (h.magic == kPlanMagic) & (h.total_q == p.total_q) & (h.total_k == p.total_k) &
+                  (h.batch == p.batch) & (h.n_rep == p.n_rep) & (h.hkv == p.hkv) & (h.causal == (causal ? 1 : 0)) &
+                  (!need_kv | (h.has_kv != 0));
   if (!ok && threadIdx.x == 0) atomicOr(&p.plan->status_use, kStatusMismatch);
   return ok;
+}
+
+__device__ __forceinline__ bool plan_matches(const AttnParams& p, bool causal, bool need_kv) {
+  return plan_header_ok(plan_header(p), p, causal, need_kv);
 }
 
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,

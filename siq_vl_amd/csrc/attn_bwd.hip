@@ -99,12 +99,14 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
   // (all its kv-heads) per run, so the heaviest-first items go round the XCDs
   const int e = xcd_order(blockIdx.x, gridDim.x, p.hkv);
   const int ii = e / p.hkv, hk = e - ii * p.hkv;
+  const PlanHeader ph = plan_header(p);
   const KvItem it = p.kvitems[ii];
-  // every field loaded before the idle test (the compiler would otherwise
-  // fetch b alone, wait for it, then fetch the rest)
+  // every field of the entry and the plan header loaded before the idle
+  // test (the compiler would otherwise fetch b alone, wait for it, then
+  // fetch the rest)
   asm volatile("" : : "s"(it.s.q_start), "s"(it.s.q_len), "s"(it.s.k_start), "s"(it.s.k_len), "s"(it.t), "s"(it.s0),
-               "s"(it.s1));
-  if (!plan_matches(p, CAUSAL, true) || it.b < 0) return;
+               "s"(it.s1), "v"(ph.magic));
+  if (!plan_header_ok(ph, p, CAUSAL, true) || it.b < 0) return;
   const SeqInfo si = it.s;
   const int k0 = it.t * BN;
   const int kb = k0 + 32 * kq;  // first kv row of this wave
@@ -434,10 +436,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_w4_kernel(const AttnPara
   // (all its kv-heads) per run, so the heaviest-first items go round the XCDs
   const int e = xcd_order(blockIdx.x, gridDim.x, p.hkv);
   const int ii = e / p.hkv, hk = e - ii * p.hkv;
+  const PlanHeader ph = plan_header(p);
   const KvItem it = p.kvitems[ii];
   asm volatile("" : : "s"(it.s.q_start), "s"(it.s.q_len), "s"(it.s.k_start), "s"(it.s.k_len), "s"(it.t), "s"(it.s0),
-               "s"(it.s1));
-  if (!plan_matches(p, CAUSAL, true) || it.b < 0) return;
+               "s"(it.s1), "v"(ph.magic));
+  if (!plan_header_ok(ph, p, CAUSAL, true) || it.b < 0) return;
   const SeqInfo si = it.s;
   const int k0 = it.t * BN;
   const int kb = k0 + 32 * wu;  // first kv row of this wave
@@ -740,11 +743,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
   // tiles, one per run, so the heaviest-first tiles go round the XCDs
   const int e = xcd_order(blockIdx.x, gridDim.x, p.hq);
   const int ti = e / p.hq, hqi = e - ti * p.hq, hk = hqi / p.n_rep;
+  const PlanHeader ph = plan_header(p);
   const QTile tl = p.qtiles[ti];
-  // every field loaded before the idle test (the compiler would otherwise
-  // fetch b alone, wait for it, then fetch the rest)
-  asm volatile("" : : "s"(tl.s.q_start), "s"(tl.s.q_len), "s"(tl.s.k_start), "s"(tl.s.k_len), "s"(tl.t));
-  if (!plan_matches(p, CAUSAL, false) || tl.b < 0) return;
+  // every field of the entry and the plan header loaded before the idle
+  // test (the compiler would otherwise fetch b alone, wait for it, then
+  // fetch the rest)
+  asm volatile("" : : "s"(tl.s.q_start), "s"(tl.s.q_len), "s"(tl.s.k_start), "s"(tl.s.k_len), "s"(tl.t),
+               "v"(ph.magic));
+  if (!plan_header_ok(ph, p, CAUSAL, false) || tl.b < 0) return;
   const SeqInfo si = tl.s;
   const int q0 = tl.t * BM;
   const int off = si.k_len - si.q_len;
@@ -755,16 +761,32 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
   const int qrow = q0 + 32 * g + l32;
   const bool qvalid = qrow < si.q_len;
   const int lim = CAUSAL ? min(si.k_len - 1, qrow + off) : si.k_len - 1;  // last kv row qrow sees
+  const bf16* kbase = p.k + (int64_t)si.k_start * p.k_tok + (int64_t)hk * p.k_head;
+  const bf16* vbase = p.v + (int64_t)si.k_start * p.v_tok + (int64_t)hk * p.v_head;
+  // loads untracked: the block loop's wait_vmem + barrier order them
+  auto issue = [&](int kb, int buf) {
+    kt.template issue<true>(kbase + (int64_t)(kb * BN) * p.k_tok, p.k_tok, si.k_len - kb * BN, smem + buf * STAGE, g);
+    vt.template issue<true>(vbase + (int64_t)(kb * BN) * p.v_tok, p.v_tok, si.k_len - kb * BN,
+                            smem + buf * STAGE + TE, g);
+  };
+  // The first K / V block goes out before this lane's rows: the wait the
+  // compiler puts before the first use of the rows also covers it, and the
+  // two latencies overlap.
+  if (nblk > 0) issue(0, 0);
+
   bf16x8 qf[D / 16], gf[D / 16];
   float lse2, dlt;
+  const int64_t lidx = (int64_t)hqi * p.lse_head + si.q_start + (qvalid ? qrow : 0);
   {
     // Q and dO of this lane's row (half h of its d), and the row's
     // Delta = rowsum(dO o O) and LSE * log2(e), which this kernel also
-    // publishes for the dK/dV kernel that runs after it
+    // publishes for the dK/dV kernel that runs after it (at its end, so that
+    // the stores do not join the first block's wait)
     const int64_t r = si.q_start + (qvalid ? qrow : 0);
     const bf16* qp = p.q + r * p.q_tok + (int64_t)hqi * p.q_head + 8 * h;
     const bf16* gp = p.dout + r * p.do_tok + (int64_t)hqi * p.do_head + 8 * h;
     const bf16* op = p.o + r * p.o_tok + (int64_t)hqi * p.o_head + 8 * h;
+    const float l2 = p.lse[lidx] * kLog2e;
     float acc = 0.f;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
@@ -775,12 +797,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
       for (int i = 0; i < 8; ++i) acc = __builtin_fmaf((float)b[i], (float)o[i], acc);
     }
     acc += __shfl_xor(acc, 32);
-    const int64_t idx = (int64_t)hqi * p.lse_head + r;
-    const float l2 = p.lse[idx] * kLog2e;
-    if (qvalid && h == 0) {
-      p.delta[idx] = acc;
-      p.lse2[idx] = l2;
-    }
     lse2 = qvalid ? l2 : INFINITY;
     dlt = qvalid ? acc : 0.f;
   }
@@ -789,15 +805,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
 #pragma unroll
   for (int i = 0; i < NDT; ++i) dq[i] = zero16();
 
-  const bf16* kbase = p.k + (int64_t)si.k_start * p.k_tok + (int64_t)hk * p.k_head;
-  const bf16* vbase = p.v + (int64_t)si.k_start * p.v_tok + (int64_t)hk * p.v_head;
-  // loads untracked: the block loop's wait_vmem + barrier order them
-  auto issue = [&](int kb, int buf) {
-    kt.template issue<true>(kbase + (int64_t)(kb * BN) * p.k_tok, p.k_tok, si.k_len - kb * BN, smem + buf * STAGE, g);
-    vt.template issue<true>(vbase + (int64_t)(kb * BN) * p.v_tok, p.v_tok, si.k_len - kb * BN,
-                            smem + buf * STAGE + TE, g);
-  };
-  if (nblk > 0) issue(0, 0);
   wait_vmem();
   __syncthreads();
 
@@ -876,6 +883,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
     __syncthreads();
   }
 
+  if (qvalid && h == 0) {
+    p.delta[lidx] = dlt;
+    p.lse2[lidx] = lse2;
+  }
   if (qvalid) {
     const int64_t r = si.q_start + qrow;
     bf16* dqp = p.dq + r * p.dq_tok + (int64_t)hqi * p.dq_head;

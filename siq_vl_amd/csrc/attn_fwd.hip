@@ -70,11 +70,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   // turn (longer runs hand the first XCD the heaviest tiles of every round)
   const int e = xcd_order(blockIdx.x, gridDim.x, p.hq);
   const int ti = e / p.hq, hqi = e - ti * p.hq, hk = hqi / p.n_rep;
+  const PlanHeader ph = plan_header(p);
   const QTile tl = p.qtiles[ti];
-  // every field loaded before the idle test (the compiler would otherwise
-  // fetch b alone, wait for it, then fetch the rest)
-  asm volatile("" : : "s"(tl.s.q_start), "s"(tl.s.q_len), "s"(tl.s.k_start), "s"(tl.s.k_len), "s"(tl.t));
-  if (!plan_matches(p, CAUSAL, false) || tl.b < 0) return;
+  // every field of the entry and the plan header loaded before the idle
+  // test (the compiler would otherwise fetch b alone, wait for it, then
+  // fetch the rest)
+  asm volatile("" : : "s"(tl.s.q_start), "s"(tl.s.q_len), "s"(tl.s.k_start), "s"(tl.s.k_len), "s"(tl.t),
+               "v"(ph.magic));
+  if (!plan_header_ok(ph, p, CAUSAL, false) || tl.b < 0) return;
   const SeqInfo si = tl.s;
   const int q0 = tl.t * BM;
   const int off = si.k_len - si.q_len;
