@@ -727,6 +727,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
   constexpr int TE = Tile::ELEMS, STAGE = 2 * TE;  // K, V
   constexpr int NDT = D / 32;
   __shared__ __align__(16) bf16 smem[2 * STAGE];
+  __shared__ __align__(16) float dsh[BM];  // Delta of the tile's rows, handed from the row pass to the MFMA layout
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int g = wave_uniform(tid >> 6);  // q group: rows 32 g .. 32 g + 31 of the tile
@@ -769,37 +770,69 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
     vt.template issue<true>(vbase + (int64_t)(kb * BN) * p.v_tok, p.v_tok, si.k_len - kb * BN,
                             smem + buf * STAGE + TE, g);
   };
-  // The first K / V block goes out before this lane's rows: the wait the
-  // compiler puts before the first use of the rows also covers it, and the
-  // two latencies overlap.
-  if (nblk > 0) issue(0, 0);
-
-  bf16x8 qf[D / 16], gf[D / 16];
-  float lse2, dlt;
-  const int64_t lidx = (int64_t)hqi * p.lse_head + si.q_start + (qvalid ? qrow : 0);
+  // Q and dO of the tile go through LDS (the two K / V stages, free until
+  // the first block is loaded): the direct loads read whole 256-byte rows,
+  // where loading the MFMA operand layout straight into registers touches 32
+  // rows per instruction.  O is only needed for Delta = rowsum(dO o O): it
+  // is read the same whole-row way into registers and multiplied with the
+  // staged dO chunk by chunk.  Each wave stages and reads back its own 32
+  // rows, so only its own load wait orders them.
+  using QStage = LdsTile<BM, D, NT / 64>;
+  static_assert(QStage::ELEMS == STAGE && QStage::PERW * QStage::RPI == 32,
+                "a q tile fills one K / V stage, and each wave stages its own 32 rows");
+  bf16* Qst = smem;
+  bf16* Gst = smem + STAGE;
   {
-    // Q and dO of this lane's row (half h of its d), and the row's
-    // Delta = rowsum(dO o O) and LSE * log2(e), which this kernel also
-    // publishes for the dK/dV kernel that runs after it (at its end, so that
-    // the stores do not join the first block's wait)
-    const int64_t r = si.q_start + (qvalid ? qrow : 0);
-    const bf16* qp = p.q + r * p.q_tok + (int64_t)hqi * p.q_head + 8 * h;
-    const bf16* gp = p.dout + r * p.do_tok + (int64_t)hqi * p.do_head + 8 * h;
-    const bf16* op = p.o + r * p.o_tok + (int64_t)hqi * p.o_head + 8 * h;
-    const float l2 = p.lse[lidx] * kLog2e;
+    QStage qs;
+    qs.init(p.q_tok, lane);
+    qs.template issue<true>(p.q + (int64_t)(si.q_start + q0) * p.q_tok + (int64_t)hqi * p.q_head, p.q_tok,
+                            si.q_len - q0, Qst, g);
+    QStage gs;
+    gs.init(p.do_tok, lane);
+    gs.template issue<true>(p.dout + (int64_t)(si.q_start + q0) * p.do_tok + (int64_t)hqi * p.do_head, p.do_tok,
+                            si.q_len - q0, Gst, g);
+  }
+  RowSpan<D> rs;
+  rs.init(lane);
+  bf16x8 ov[RowSpan<D>::N32];
+  {
+    const bf16* obase = p.o + (int64_t)si.q_start * p.o_tok + (int64_t)hqi * p.o_head + 8 * rs.c;
+#pragma unroll
+    for (int i = 0; i < RowSpan<D>::N32; ++i) {
+      const int r = min(q0 + rs.row(32 * g, i), si.q_len - 1);  // rows past the end re-read the last one
+      ov[i] = ld_bf16x8(obase + (int64_t)r * p.o_tok);
+    }
+  }
+  const int64_t lidx = (int64_t)hqi * p.lse_head + si.q_start + (qvalid ? qrow : 0);
+  const float l2 = p.lse[lidx] * kLog2e;
+  wait_vmem();
+  asm volatile("" ::: "memory");  // the LDS reads below stay after the wait
+  // Delta of each of the wave's rows: the CH lanes of a row sum their chunks
+  // (in the order d = 8 c + i, then the lanes' partial sums pairwise), and
+  // one of them hands it on through LDS to the lane that owns the row
+#pragma unroll
+  for (int i = 0; i < RowSpan<D>::N32; ++i) {
+    const int r = rs.row(32 * g, i);
+    const bf16x8 gv = ld_bf16x8(Gst + rs.lds(r));
     float acc = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-      const bf16x8 a = ld_bf16x8(qp + 16 * ks), b = ld_bf16x8(gp + 16 * ks), o = ld_bf16x8(op + 16 * ks);
-      qf[ks] = qvalid ? a : zero_bf16x8();
-      gf[ks] = qvalid ? b : zero_bf16x8();
+    for (int k = 0; k < 8; ++k) acc = __builtin_fmaf((float)gv[k], (float)ov[i][k], acc);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc = __builtin_fmaf((float)b[i], (float)o[i], acc);
-    }
-    acc += __shfl_xor(acc, 32);
-    lse2 = qvalid ? l2 : INFINITY;
-    dlt = qvalid ? acc : 0.f;
+    for (int o = 1; o < RowSpan<D>::CH; o <<= 1) acc += __shfl_xor(acc, o);
+    if (rs.c == 0) dsh[r] = acc;
   }
+  bf16x8 qf[D / 16], gf[D / 16];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) {
+    const bf16x8 a = rr.read(Qst, 32 * g, ks), b = rr.read(Gst, 32 * g, ks);
+    qf[ks] = qvalid ? a : zero_bf16x8();
+    gf[ks] = qvalid ? b : zero_bf16x8();
+  }
+  const float lse2 = qvalid ? l2 : INFINITY;
+  const float dlt = qvalid ? dsh[32 * g + l32] : 0.f;
+  // every wave's staged rows read: the first K / V block may overwrite them
+  __syncthreads();
+  if (nblk > 0) issue(0, 0);
 
   f32x16 dq[NDT];
 #pragma unroll
@@ -887,21 +920,34 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
     p.delta[lidx] = dlt;
     p.lse2[lidx] = lse2;
   }
-  if (qvalid) {
+  if constexpr (!ROPE) {
+    // dq through LDS, so that it leaves as whole 256-byte rows: after the
+    // block loop's last barrier no wave reads K / V, and each wave writes and
+    // reads back only its own 32 rows (no barrier).  Lane (l32, h) holds
+    // d = 32 dt + 16 j + 8 h + i of its row: logical chunk 4 dt + 2 j + h.
+    RowWrite<D> rw;
+    rw.init(lane);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        bf16x8 a;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = (bf16)(dq[dt][8 * j + i] * p.scale);
+        rw.write(smem, 32 * g, 4 * dt + 2 * j + h, a);
+      }
+    }
+    bf16* dbase = p.dq + (int64_t)(si.q_start + q0) * p.dq_tok + (int64_t)hqi * p.dq_head + 8 * rs.c;
+#pragma unroll
+    for (int i = 0; i < RowSpan<D>::N32; ++i) {
+      const int r = rs.row(32 * g, i);
+      const bf16x8 v = ld_bf16x8(smem + rs.lds(r));
+      if (q0 + r < si.q_len) st_bf16x8(dbase + (int64_t)r * p.dq_tok, v);
+    }
+  } else if (qvalid) {
     const int64_t r = si.q_start + qrow;
     bf16* dqp = p.dq + r * p.dq_tok + (int64_t)hqi * p.dq_head;
-    if constexpr (!ROPE) {
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          bf16x8 a;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) a[i] = (bf16)(dq[dt][8 * j + i] * p.scale);
-          st_bf16x8(dqp + 32 * dt + 16 * j + 8 * h, a);
-        }
-      }
-    } else {
+    {
       // dq of the q before rotation: the gradient of the rotated q, rounded
       // to bf16 as the attention's own output would be, through the
       // rotation's backward.  Lane holds d = 32 dt + 16 j + 8 h + i; the
@@ -939,31 +985,31 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
 
 // Atomic backward, before the dK/dV kernel: Delta = rowsum(dO o O) and LSE *
 // log2(e) of every (row, q-head), which the dQ kernel publishes in the
-// deterministic backward, and the fp32 dQ sums cleared.  Two lanes per (row,
-// head), lane h summing d = 16 ks + 8 h + i in the dQ kernel's order, so that
-// Delta -- and with it dK and dV -- is bitwise that of the deterministic
+// deterministic backward, and the fp32 dQ sums cleared.  D / 8 lanes per
+// (row, head), lane c summing the 8 elements of chunk c in order and the
+// lanes' sums added pairwise (xor 1, 2, 4, ...), as the dQ kernel does, so
+// that Delta -- and with it dK and dV -- is bitwise that of the deterministic
 // backward.
 template <int D>
 __global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const AttnParams p) {
-  const int h = threadIdx.x & 1;
+  constexpr int LP = D / 8, PPB = 256 / LP;  // lanes per (row, head), pairs per block
+  const int c = threadIdx.x % LP;
   const int64_t npairs = p.total_q * p.hq;
-  for (int64_t pi = (int64_t)blockIdx.x * 128 + (threadIdx.x >> 1); pi < npairs; pi += (int64_t)gridDim.x * 128) {
+  // the lanes of a pair share pi, so they take the same trips and the shuffles below stay within active pairs
+  for (int64_t pi = (int64_t)blockIdx.x * PPB + threadIdx.x / LP; pi < npairs; pi += (int64_t)gridDim.x * PPB) {
     const int64_t row = pi / p.hq;
     const int hq = (int)(pi - row * p.hq);
-    const bf16* op = p.o + row * p.o_tok + (int64_t)hq * p.o_head + 8 * h;
-    const bf16* gp = p.dout + row * p.do_tok + (int64_t)hq * p.do_head + 8 * h;
-    float* z = p.dq_acc + pi * D + 8 * h;
+    const bf16x8 o = ld_bf16x8(p.o + row * p.o_tok + (int64_t)hq * p.o_head + 8 * c);
+    const bf16x8 g = ld_bf16x8(p.dout + row * p.do_tok + (int64_t)hq * p.do_head + 8 * c);
     float acc = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-      const bf16x8 o = ld_bf16x8(op + 16 * ks), g = ld_bf16x8(gp + 16 * ks);
+    for (int i = 0; i < 8; ++i) acc = __builtin_fmaf((float)g[i], (float)o[i], acc);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc = __builtin_fmaf((float)g[i], (float)o[i], acc);
-      *reinterpret_cast<f32x4*>(z + 16 * ks) = f32x4{0.f, 0.f, 0.f, 0.f};
-      *reinterpret_cast<f32x4*>(z + 16 * ks + 4) = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    acc += __shfl_xor(acc, 1);
-    if (h == 0) {
+    for (int k = 1; k < LP; k <<= 1) acc += __shfl_xor(acc, k);
+    float* z = p.dq_acc + pi * D + 8 * c;
+    *reinterpret_cast<f32x4*>(z) = f32x4{0.f, 0.f, 0.f, 0.f};
+    *reinterpret_cast<f32x4*>(z + 4) = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (c == 0) {
       const int64_t idx = (int64_t)hq * p.lse_head + row;
       p.delta[idx] = acc;
       p.lse2[idx] = p.lse[idx] * kLog2e;
@@ -1000,7 +1046,8 @@ hipError_t launch_bwd_t(const AttnParams& p, int qcap, int kvcap, hipStream_t st
   if (p.dq_acc != nullptr) {
     // atomic: Delta / LSE2 and cleared sums, dK/dV with dQ, partial sums, dq
     const int64_t pairs = p.total_q * p.hq;
-    const int64_t pblocks = std::min<int64_t>((pairs + 127) / 128, 8192);
+    const int64_t ppb = 256 / (D / 8);  // (row, head) pairs per prep block
+    const int64_t pblocks = std::min<int64_t>((pairs + ppb - 1) / ppb, 8192);
     const int64_t blocks = std::min<int64_t>((pairs + 256 / (D / 8) - 1) / (256 / (D / 8)), 8192);
     if (pblocks > 0) hipLaunchKernelGGL((attn_bwd_prep_kernel<D>), dim3((unsigned)pblocks), dim3(256), 0, stream, p);
     hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, CAUSAL, true>), kvgrid, dim3(512), 0, stream, p);

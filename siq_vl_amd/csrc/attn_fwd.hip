@@ -100,7 +100,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
     vt.template issue<true>(vbase, p.v_tok, si.k_len, smem + TE, wu);
   }
   bf16x8 qf[D / 16];
-  {
+  using QStage = LdsTile<BM, D, NT / 64>;
+  static_assert(QStage::ELEMS == STAGE && QStage::PERW * QStage::RPI == 32,
+                "the q tile fills one K / V stage, and each wave stages its own 32 rows");
+  if constexpr (!ROPE) {
+    // The q tile goes through LDS, in the second K / V stage (free until the
+    // first prefetch of the block loop): the direct loads read whole
+    // 256-byte rows, where loading the MFMA operand layout straight into
+    // registers touches 32 rows per instruction.  Each wave stages its own 32
+    // rows and reads them back after its own load wait.
+    QStage qs;
+    qs.init(p.q_tok, lane);
+    qs.template issue<true>(p.q + (int64_t)(si.q_start + q0) * p.q_tok + (int64_t)hqi * p.q_head, p.q_tok,
+                            si.q_len - q0, smem + STAGE, wu);
+  } else {
     const int64_t r = si.q_start + (qvalid ? qrow : 0);
     const bf16* qp = p.q + r * p.q_tok + (int64_t)hqi * p.q_head + 8 * h;
 #pragma unroll
@@ -149,6 +162,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   float mref = -INFINITY, msafe = 0.f, lsum = 0.f;  // lsum: this lane's partial row sum
 
   wait_vmem();
+  asm volatile("" ::: "memory");  // the LDS reads below stay after the wait
+  if constexpr (!ROPE) {
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      const bf16x8 x = rr.read(smem + STAGE, 32 * w, ks);
+      qf[ks] = qvalid ? x : zero_bf16x8();
+    }
+  }
+  // every wave's rows read (the first prefetch overwrites the q stage) and
+  // the first K / V block visible
   __syncthreads();
 
   const int wq_last = q0 + 32 * w + 31;  // last q row of this wave
@@ -245,9 +268,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   }
 
   const float ltot = half_sum(lsum);
-  if (qvalid) {
+  if (qvalid && h == 0) {
+    p.lse[(int64_t)hqi * p.lse_head + si.q_start + qrow] = ltot > 0.f ? (mref + __log2f(ltot)) * kLn2 : -INFINITY;
+  }
+  // O through LDS, so that it leaves as whole 256-byte rows: after the block
+  // loop's last barrier no wave reads K / V, and each wave writes and reads
+  // back only its own 32 rows (the wave's LDS accesses run in order, so no
+  // barrier).  Lane (l32, h) holds d = 32 dt + 16 j + 8 h + i of its row:
+  // logical chunk 4 dt + 2 j + h.
+  {
     const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-    bf16* op = p.out + (int64_t)(si.q_start + qrow) * p.o_tok + (int64_t)hqi * p.o_head;
+    RowWrite<D> rw;
+    rw.init(lane);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
@@ -255,12 +287,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
         bf16x8 ov;
 #pragma unroll
         for (int i = 0; i < 8; ++i) ov[i] = (bf16)(oacc[dt][8 * j + i] * inv);
-        st_bf16x8(op + 32 * dt + 16 * j + 8 * h, ov);
+        rw.write(smem, 32 * w, 4 * dt + 2 * j + h, ov);
       }
     }
-    if (h == 0) {
-      p.lse[(int64_t)hqi * p.lse_head + si.q_start + qrow] =
-          ltot > 0.f ? (mref + __log2f(ltot)) * kLn2 : -INFINITY;
+    RowSpan<D> rs;
+    rs.init(lane);
+    bf16* obase = p.out + (int64_t)(si.q_start + q0) * p.o_tok + (int64_t)hqi * p.o_head + 8 * rs.c;
+#pragma unroll
+    for (int i = 0; i < RowSpan<D>::N32; ++i) {
+      const int r = rs.row(32 * w, i);
+      const bf16x8 v = ld_bf16x8(smem + rs.lds(r));
+      if (q0 + r < si.q_len) st_bf16x8(obase + (int64_t)r * p.o_tok, v);
     }
   }
 }

@@ -138,6 +138,40 @@ struct RowRead {
   }
 };
 
+// Writes in the staging layout from the MFMA row layout: lane l owns tile row
+// rb + l % 32 (rb a multiple of 32) and writes its 16-byte logical chunks c,
+// so that whole rows can then be read out 256 bytes at a time (RowSpan).
+template <int D>
+struct RowWrite {
+  uint32_t base;
+  int s;
+  __device__ __forceinline__ void init(int lane) {
+    const int l32 = lane & 31;
+    base = (uint32_t)(l32 * D);
+    s = swz<D>(l32);
+  }
+  __device__ __forceinline__ void write(bf16* T, int rb, int c, const bf16x8& v) const {
+    st_bf16x8(T + rb * D + base + 8 * (c ^ s), v);
+  }
+};
+
+// Whole-row access to a staged tile: instruction i of a wave covers tile rows
+// rb + RPI i .. rb + RPI i + RPI - 1, lane l taking row rb + RPI i + l / CH and
+// logical chunk l % CH, so each instruction reads or writes RPI whole rows of
+// global memory (N32 instructions cover the wave's 32 rows).
+template <int D>
+struct RowSpan {
+  static constexpr int CH = D / 8, RPI = 64 / CH, N32 = 32 / RPI;
+  int lr, c;
+  __device__ __forceinline__ void init(int lane) {
+    lr = lane / CH;
+    c = lane % CH;
+  }
+  __device__ __forceinline__ int row(int rb, int i) const { return rb + RPI * i + lr; }
+  // element offset of this lane's chunk of tile row r in the staging layout
+  __device__ __forceinline__ uint32_t lds(int r) const { return (uint32_t)(r * D + 8 * (c ^ swz<D>(r))); }
+};
+
 // Transposed operand reads with ds_read_b64_tr_b16.  Within each 16-lane
 // group, lane p = 4j + q supplies the address of row j of a 4 x 16 block
 // (8 bytes at column group q) and lane i receives element i % 4 of the chunks
