@@ -347,28 +347,54 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
     __syncthreads();
   }
 
-  // Sum the two q-group waves' partial dK^T (then dV^T) of each kv quarter
-  // through LDS; wave g of a quarter then owns d-tiles g, g + 2, ...  A whole
-  // tile (np == 1) is scaled and written as bf16; a piece of a split tile
-  // writes its fp32 sums to its slot ([dK | dV][kv row][d]) for
+  // Sum the two q-group waves' partial dK^T / dV^T of each kv quarter in one
+  // exchange through LDS: wave g finishes d-tiles [g NDT / 2, (g + 1) NDT / 2)
+  // of both tensors and hands the other half of its partials to its partner
+  // (wave 1 - g of the quarter), with 16-byte LDS stores of 1 KB per
+  // instruction.  Each sum is g = 0's partial plus g = 1's.  A whole tile
+  // (np == 1) is scaled and written as bf16; a piece of a split tile writes
+  // its fp32 sums to its slot ([dK | dV][kv row][d]) for
   // attn_bwd_dkv_sum_kernel.
-  float* red = reinterpret_cast<float*>(smem);  // [2 g][4 kq][NDT][16][64]
   const bool split = it.np > 1;
   const bool slot_ok = split && it.slot0 >= 0 && (it.slot0 + it.np) * p.hkv <= kSplitSlots;
   float* slot = p.dkv_part + (int64_t)((it.slot0 + it.piece) * p.hkv + hk) * (2 * BN * D);
   const int64_t row = si.k_start + kvrow;
-  auto reduce = [&](const f32x16 (&acc)[NDT], int which) {
+  constexpr int HT = NDT / 2;             // d-tiles a wave finishes
+  constexpr int XR = 2 * HT * 16 * 64;    // floats a wave hands its partner: [dK | dV][HT][16][64 lanes]
+  static_assert(8 * XR * 4 <= SMEM * 2, "the exchange fits the LDS");
+  float* inbox = reinterpret_cast<float*>(smem) + (2 * kq + g) * XR;
+  float* outbox = reinterpret_cast<float*>(smem) + (2 * kq + (1 - g)) * XR;
+  // the step loop ends on a barrier; an item without steps has only read K / V (D = 64) since the last one
+  if (ns == 0) __syncthreads();
+  // d-tiles are indexed statically (a wave-uniform branch picks them), so
+  // the accumulators stay in registers
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+  for (int t = 0; t < NDT; ++t) {
+    if (t / HT == g) continue;  // this wave finishes tile t itself
+    const int u = t % HT;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[(((g * 4 + kq) * NDT + dt) * 16 + r) * 64 + lane] = acc[dt][r];
-    __syncthreads();
-    for (int dt = g; dt < NDT; dt += 2) {
+    for (int q4 = 0; q4 < 4; ++q4) {
+      *reinterpret_cast<f32x4*>(outbox + ((0 * HT + u) * 4 + q4) * 256 + 4 * lane) =
+          f32x4{dk[t][4 * q4], dk[t][4 * q4 + 1], dk[t][4 * q4 + 2], dk[t][4 * q4 + 3]};
+      *reinterpret_cast<f32x4*>(outbox + ((1 * HT + u) * 4 + q4) * 256 + 4 * lane) =
+          f32x4{dv[t][4 * q4], dv[t][4 * q4 + 1], dv[t][4 * q4 + 2], dv[t][4 * q4 + 3]};
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int which = 0; which < 2; ++which) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      if (dt / HT != g) continue;  // the partner finishes tile dt
+      const int u = dt % HT;
+      const f32x16& mine = which == 0 ? dk[dt] : dv[dt];
       float sum[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        sum[r] = red[(((0 * 4 + kq) * NDT + dt) * 16 + r) * 64 + lane] +
-                 red[(((1 * 4 + kq) * NDT + dt) * 16 + r) * 64 + lane];
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const f32x4 o = *reinterpret_cast<const f32x4*>(inbox + ((which * HT + u) * 4 + q4) * 256 + 4 * lane);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sum[4 * q4 + i] = g == 0 ? mine[4 * q4 + i] + o[i] : o[i] + mine[4 * q4 + i];
+      }
       if (!split) {
         if (kvvalid) {
           bf16* dst = which == 0 ? p.dk + row * p.dk_tok + (int64_t)hk * p.dk_head
@@ -392,10 +418,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnParams 
         }
       }
     }
-    __syncthreads();
-  };
-  reduce(dk, 0);
-  reduce(dv, 1);
+  }
 }
 
 // dK/dV with one wave per SIMD (the deterministic backward's kernel at D =
