@@ -583,7 +583,7 @@ def bench_splice(steps: int, warmup: int) -> dict:
             "table_bytes": table_bytes, "table_gbs": table_bytes / (table_ms * 1e-3) / 1e9}
 
 
-def bench_ce(steps: int, warmup: int, chunk: int | None) -> dict:
+def bench_ce(steps: int, warmup: int, chunk: int | None, modes=("full", "dh_only")) -> dict:
     cfg = W.CONFIG4
     dev = torch.device("cuda")
     x = W.ce_inputs(cfg, device=dev)
@@ -597,8 +597,10 @@ def bench_ce(steps: int, warmup: int, chunk: int | None) -> dict:
         # targets): loss and dHidden only, no dW GEMM
         return C.flce_fwd_bwd(x["hidden"], x["weight"], x["labels"], need_dweight=False, chunk_tokens=chunk)
 
-    r = timed_steps([("ce", step)], steps, warmup)
-    r_dh = timed_steps([("ce_dh", step_dh)], steps, warmup)
+    r = timed_steps([("ce", step)], steps, warmup) if "full" in modes else None
+    r_dh = timed_steps([("ce_dh", step_dh)], steps, warmup) if "dh_only" in modes else None
+    if r is None:  # the dH-only leg alone (a profiling aid)
+        return {"dh_only_ms": r_dh["median_ms"], "chunk": chunk}
     ms = r["median_ms"]
     # tokens/s counts every row of the batch (the metric); the executed TFLOP/s counts the work the
     # kernels run: rows whose label is ignored are compacted out before the logits GEMM
@@ -610,7 +612,7 @@ def bench_ce(steps: int, warmup: int, chunk: int | None) -> dict:
         "tflops_all_rows": 6.0 * cfg.n * cfg.hdim * cfg.vocab / (ms * 1e-3) / 1e12,
         "tflops_executed": 6.0 * n_valid * cfg.hdim * cfg.vocab / (ms * 1e-3) / 1e12,
         "chunk": chunk, "workspace_bytes": ws,
-        "dh_only_ms": r_dh["median_ms"], "dh_only_workspace_bytes": C.flce_workspace_bytes(cfg.n, cfg.hdim, cfg.vocab, chunk, False),
+        "dh_only_ms": r_dh["median_ms"] if r_dh else None, "dh_only_workspace_bytes": C.flce_workspace_bytes(cfg.n, cfg.hdim, cfg.vocab, chunk, False),
         "e_bytes": 2 * chunk * cfg.vocab,
         "algorithmic_bytes": 2 * (2 * cfg.n * cfg.hdim + 2 * cfg.vocab * cfg.hdim) + 8 * cfg.n,
     }
@@ -744,8 +746,8 @@ def main() -> int:
     ap.add_argument("--skip-projector", action="store_true")
     ap.add_argument("--skip-splice", action="store_true")
     ap.add_argument("--attn-only", action="store_true", help="attention configs only (no CE / widening legs)")
-    ap.add_argument("--leg", choices=["attn1", "attn2", "attn3", "attn5", "attn6", "ce", "rope", "rope_attn", "proj",
-                                      "splice"],
+    ap.add_argument("--leg", choices=["attn1", "attn2", "attn3", "attn5", "attn6", "ce", "ce_dh", "rope", "rope_attn",
+                                      "proj", "splice"],
                     default=None,
                     help="run one leg only and print its timings (a profiling aid: one rocprofv3 counter pass per "
                          "leg attributes every dispatch to its workload); no contract JSON line")
@@ -778,7 +780,8 @@ def main() -> int:
                "attn3": lambda: bench_attention(3, steps, args.warmup),
                "attn5": lambda: bench_attention(5, steps, args.warmup),
                "attn6": lambda: bench_attention(6, steps, args.warmup),
-               "ce": lambda: bench_ce(steps, args.warmup, args.ce_chunk),
+               "ce": lambda: bench_ce(steps, args.warmup, args.ce_chunk, modes=("full",)),
+               "ce_dh": lambda: bench_ce(steps, args.warmup, args.ce_chunk, modes=("dh_only",)),
                "rope": lambda: bench_rope(steps, args.warmup),
                "rope_attn": lambda: bench_rope_attention(steps, args.warmup),
                "proj": lambda: bench_projector(steps, args.warmup),

@@ -943,65 +943,46 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnParams p)
     p.delta[lidx] = dlt;
     p.lse2[lidx] = lse2;
   }
-  if constexpr (!ROPE) {
-    // dq through LDS, so that it leaves as whole 256-byte rows: after the
-    // block loop's last barrier no wave reads K / V, and each wave writes and
-    // reads back only its own 32 rows (no barrier).  Lane (l32, h) holds
-    // d = 32 dt + 16 j + 8 h + i of its row: logical chunk 4 dt + 2 j + h.
-    RowWrite<D> rw;
-    rw.init(lane);
+  // dq through LDS, so that it leaves as whole 256-byte rows: after the
+  // block loop's last barrier no wave reads K / V, and each wave writes and
+  // reads back only its own 32 rows (no barrier).  Lane (l32, h) holds
+  // d = 32 dt + 16 j + 8 h + i of its row: logical chunk 4 dt + 2 j + h.  The
+  // staged values are bf16(scale * dQ), the attention's own output rounding.
+  RowWrite<D> rw;
+  rw.init(lane);
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
+  for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        bf16x8 a;
+    for (int j = 0; j < 2; ++j) {
+      bf16x8 a;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) a[i] = (bf16)(dq[dt][8 * j + i] * p.scale);
-        rw.write(smem, 32 * g, 4 * dt + 2 * j + h, a);
-      }
+      for (int i = 0; i < 8; ++i) a[i] = (bf16)(dq[dt][8 * j + i] * p.scale);
+      rw.write(smem, 32 * g, 4 * dt + 2 * j + h, a);
     }
-    bf16* dbase = p.dq + (int64_t)(si.q_start + q0) * p.dq_tok + (int64_t)hqi * p.dq_head + 8 * rs.c;
+  }
+  bf16* dbase = p.dq + (int64_t)(si.q_start + q0) * p.dq_tok + (int64_t)hqi * p.dq_head + 8 * rs.c;
 #pragma unroll
-    for (int i = 0; i < RowSpan<D>::N32; ++i) {
-      const int r = rs.row(32 * g, i);
-      const bf16x8 v = ld_bf16x8(smem + rs.lds(r));
-      if (q0 + r < si.q_len) st_bf16x8(dbase + (int64_t)r * p.dq_tok, v);
-    }
-  } else if (qvalid) {
-    const int64_t r = si.q_start + qrow;
-    bf16* dqp = p.dq + r * p.dq_tok + (int64_t)hqi * p.dq_head;
-    {
-      // dq of the q before rotation: the gradient of the rotated q, rounded
-      // to bf16 as the attention's own output would be, through the
-      // rotation's backward.  Lane holds d = 32 dt + 16 j + 8 h + i; the
-      // partner d + D / 2 is d-tile dt + NDT / 2 of the same lane.
-      // (cos / sin held through the kv loop would not fit the registers)
-      const bf16* cp = p.rcos + r * p.rc_tok + 8 * h;
-      const bf16* sp = p.rsin + r * p.rs_tok + 8 * h;
-      bf16x8 rc[D / 16], rs[D / 16];
-#pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) {
-        rc[ks] = ld_bf16x8(cp + 16 * ks);
-        rs[ks] = ld_bf16x8(sp + 16 * ks);
-      }
-#pragma unroll
-      for (int dt = 0; dt < NDT / 2; ++dt) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          bf16x8 g1, g2;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            g1[i] = (bf16)(dq[dt][8 * j + i] * p.scale);
-            g2[i] = (bf16)(dq[dt + NDT / 2][8 * j + i] * p.scale);
-          }
-          // chunk 2 dt + j holds d0 .. d0 + 7 (+ 8 h); the partner is chunk 2 dt + j + D / 32
-          const int d0 = 32 * dt + 16 * j, c0 = 2 * dt + j;
-          bf16x8 o1, o2;
-          rope_bwd8(g1, g2, rc[c0], rc[c0 + D / 32], rs[c0], rs[c0 + D / 32], o1, o2);
-          st_bf16x8(dqp + d0 + 8 * h, o1);
-          st_bf16x8(dqp + d0 + D / 2 + 8 * h, o2);
-        }
-      }
+  for (int i = 0; i < RowSpan<D>::N32; ++i) {
+    const int r = rs.row(32 * g, i);
+    const bf16x8 v = ld_bf16x8(smem + rs.lds(r));
+    if (q0 + r >= si.q_len) continue;
+    if constexpr (!ROPE) {
+      st_bf16x8(dbase + (int64_t)r * p.dq_tok, v);
+    } else {
+      // dq of the q before rotation, through the rotation's backward (the
+      // separate RoPE backward pass's roundings): d pairs with d + D / 2, so
+      // chunk c with chunk c ^ CH / 2, read back from the staged row
+      constexpr int HC = RowSpan<D>::CH / 2;
+      const bool lo = rs.c < HC;
+      const int cl = lo ? rs.c : rs.c - HC;
+      const bf16x8 w = ld_bf16x8(smem + (uint32_t)(r * D + 8 * ((rs.c ^ HC) ^ swz<D>(r))));
+      const int64_t tok = si.q_start + q0 + r;
+      const bf16* cp = p.rcos + tok * p.rc_tok + 8 * cl;
+      const bf16* sp = p.rsin + tok * p.rs_tok + 8 * cl;
+      bf16x8 o1, o2;
+      rope_bwd8(lo ? v : w, lo ? w : v, ld_bf16x8(cp), ld_bf16x8(cp + D / 2), ld_bf16x8(sp), ld_bf16x8(sp + D / 2), o1,
+                o2);
+      st_bf16x8(dbase + (int64_t)r * p.dq_tok, lo ? o1 : o2);
     }
   }
 }
