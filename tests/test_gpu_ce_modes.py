@@ -150,3 +150,35 @@ def test_out_of_range_label_raises():
     C.check_pending_labels(block=True)
     with pytest.raises(C.LabelError):
         C.fused_linear_cross_entropy(hg, wg, y2.to(DEV), validate="sync")
+
+
+def test_capture_in_a_hip_graph_with_a_lazy_check_pending():
+    """The raw training call and the autograd op captured in a HIP graph while
+    an earlier call's lazy label check is still pending: inside the capture
+    no event is queried and no count is copied, and every replay (with eager
+    work and synchronisation between them) gives the eager call's loss, dH and
+    dW bit for bit."""
+    h, w, y = make(300, 256, 1000, seed=3)
+    print("flce graph capture n=300 V=1000", flush=True)
+    hd, wd, yd = h.to(DEV), w.to(DEV), y.to(DEV)
+    loss_e, _, _, dh_e, dw_e = C.flce_fwd_bwd(hd, wd, yd, -100, None, True, 256)
+    hg, wg = hd.clone().requires_grad_(True), wd.clone().requires_grad_(True)
+    op_e = C.fused_linear_cross_entropy(hg, wg, yd)  # leaves a lazy check pending
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up off the capture, as graphs want
+        C.flce_fwd_bwd(hd, wd, yd, -100, None, True, 256)
+        C.fused_linear_cross_entropy(hg, wg, yd)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        loss_g, _, _, dh_g, dw_g = C.flce_fwd_bwd(hd, wd, yd, -100, None, True, 256)
+        op_g = C.fused_linear_cross_entropy(hg, wg, yd)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(loss_g, loss_e) and torch.equal(dh_g, dh_e) and torch.equal(dw_g, dw_e)
+        assert torch.equal(op_g.detach(), op_e.detach())
+        (hd.float() * 2.0).sum().item()  # eager work between the replays
+    C.check_pending_labels(block=True)
