@@ -11,6 +11,9 @@
 // count needs no nonzero() on the host.
 //
 // Kernels:
+//  * splice_fused_kernel (up to kFusedMaxTokens tokens): the whole forward
+//    in one launch, each workgroup counting the image tokens before its own
+//    (below); longer batches run the next two kernels;
 //  * splice_scan_kernel (one workgroup; per round 16 chunks of 1024 tokens
 //    loaded at once, wave ballots, one prefix over the 256 (chunk, wave)
 //    counts): exclusive prefix count of image
@@ -125,6 +128,129 @@ __global__ __launch_bounds__(256) void splice_gather_kernel(const SpliceArgs a) 
     }
     bf16* dst = a.out + p * a.hidden;
     for (int64_t c = lane; c < nvec; c += 64) st_bf16x8(dst + 8 * c, src ? ld_bf16x8(src + 8 * c) : zero_bf16x8());
+  }
+}
+
+// One-kernel splice for batches of up to kFusedMaxTokens tokens (the scan
+// kernel above is a single workgroup, and waiting for it costs more than
+// counting again).  Workgroup w owns tokens [w R, w R + R), R = rpw (a
+// multiple of 64): it counts the image tokens before its first token itself
+// (every thread reads kFusedUnroll ids of the earlier tokens at a time; at
+// most kFusedMaxTokens * 8 bytes, served by L2), ranks its own image tokens
+// with wave ballots, records each row's source in LDS, then its eight waves
+// copy the rows, kFusedUnroll 16-byte chunks per lane in flight.  The last
+// workgroup reads every id, so it writes counts and fills the vision slots
+// no token took with -1.  Outputs are those of splice_scan_kernel +
+// splice_gather_kernel, bit for bit (the rank workspace is not used).
+constexpr int kFusedThreads = 512;
+constexpr int kFusedBlocks = 256;
+constexpr int64_t kFusedMaxTokens = 32768;
+constexpr int kFusedMaxRows = (int)(kFusedMaxTokens / kFusedBlocks);
+constexpr int kFusedUnroll = 8;
+static_assert(kFusedMaxRows % 64 == 0, "rows per workgroup come in waves of 64");
+
+__global__ __launch_bounds__(kFusedThreads) void splice_fused_kernel(const SpliceArgs a, int32_t* __restrict__ image_pos,
+                                                                     int64_t* __restrict__ counts, int rpw) {
+  constexpr int NWV = kFusedThreads / 64;
+  __shared__ const bf16* src_sh[kFusedMaxRows];
+  __shared__ long long red_sh[2][NWV];
+  __shared__ long long found_sh;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * rpw;
+  const bool last = blockIdx.x == gridDim.x - 1;
+  const int64_t image_id = a.image_id, vocab = a.vocab;
+
+  // image tokens (and, in the last workgroup, ids outside [0, vocab)) before r0
+  long long img = 0, bad = 0;
+  for (int64_t base = tid; base < r0; base += (int64_t)kFusedThreads * kFusedUnroll) {
+    int64_t v[kFusedUnroll];
+#pragma unroll
+    for (int u = 0; u < kFusedUnroll; ++u) {
+      const int64_t p = base + (int64_t)u * kFusedThreads;
+      v[u] = p < r0 ? a.ids[p] : image_id - 1;
+    }
+#pragma unroll
+    for (int u = 0; u < kFusedUnroll; ++u) {
+      const bool inb = base + (int64_t)u * kFusedThreads < r0;
+      img += (inb && v[u] == image_id) ? 1 : 0;
+      bad += (inb && v[u] != image_id && (v[u] < 0 || v[u] >= vocab)) ? 1 : 0;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    img += __shfl_xor(img, o);
+    bad += __shfl_xor(bad, o);
+  }
+  if (lane == 0) {
+    red_sh[0][wv] = img;
+    red_sh[1][wv] = bad;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    long long carry = 0, badt = 0;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) {
+      carry += red_sh[0][w];
+      badt += red_sh[1][w];
+    }
+    // this workgroup's tokens, 64 at a time in token order
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    for (int j = 0; j < rpw; j += 64) {
+      const int64_t p = r0 + j + lane;
+      const bool inb = p < a.n;
+      const int64_t v = inb ? a.ids[p] : image_id - 1;
+      const bool isimg = inb && v == image_id;
+      const uint64_t m = __ballot(isimg);
+      const long long r = carry + __popcll(m & below);
+      const bf16* src = nullptr;
+      if (isimg) {
+        if (r < a.n_vision) {
+          src = a.vision + r * a.hidden;
+          image_pos[r] = (int32_t)p;
+        }
+      } else if (v >= 0 && v < vocab) {
+        src = a.weight + v * a.hidden;
+      }
+      src_sh[j + lane] = src;
+      carry += __popcll(m);
+      badt += __popcll(__ballot(inb && !isimg && (v < 0 || v >= vocab)));
+    }
+    if (last && lane == 0) {
+      counts[0] = carry;
+      counts[1] = badt;
+      found_sh = carry;
+    }
+  }
+  __syncthreads();
+  if (last) {
+    for (long long r = found_sh + tid; r < a.n_vision; r += kFusedThreads) image_pos[r] = -1;
+  }
+
+  // rows: wave wv copies rows wv, wv + NWV, ... of the workgroup's rows that exist, as one list of
+  // (row, 16-byte chunk) pairs
+  const int nvec = (int)(a.hidden / 8);
+  const int nrows = (int)min<int64_t>(rpw, a.n - r0);
+  const int my_rows = nrows > wv ? (nrows - wv + NWV - 1) / NWV : 0;
+  const int total = my_rows * nvec;
+  for (int base = lane; base < total; base += 64 * kFusedUnroll) {
+    bf16x8 x[kFusedUnroll];
+#pragma unroll
+    for (int u = 0; u < kFusedUnroll; ++u) {
+      const int idx = base + 64 * u;
+      if (idx < total) {
+        const int k = idx / nvec, c = idx - k * nvec;
+        const bf16* src = src_sh[wv + NWV * k];
+        x[u] = src ? ld_bf16x8(src + 8 * c) : zero_bf16x8();
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kFusedUnroll; ++u) {
+      const int idx = base + 64 * u;
+      if (idx < total) {
+        const int k = idx / nvec, c = idx - k * nvec;
+        st_bf16x8(a.out + (r0 + wv + NWV * k) * a.hidden + 8 * c, x[u]);
+      }
+    }
   }
 }
 
@@ -344,6 +470,14 @@ unsigned row_blocks(int64_t n) {
 }  // namespace
 
 hipError_t splice_fwd(const SpliceArgs& a, int32_t* image_pos, int64_t* counts, hipStream_t stream) {
+  if (a.n > 0 && a.n <= kFusedMaxTokens) {
+    // rows per workgroup: a multiple of 64 with at most kFusedBlocks workgroups
+    const int64_t per = (a.n + kFusedBlocks - 1) / kFusedBlocks;
+    const int rpw = (int)((per + 63) / 64 * 64);
+    const unsigned blocks = (unsigned)((a.n + rpw - 1) / rpw);
+    hipLaunchKernelGGL(splice_fused_kernel, dim3(blocks), dim3(kFusedThreads), 0, stream, a, image_pos, counts, rpw);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(splice_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, a.ids, a.n, a.vocab, a.image_id,
                      a.n_vision, a.rank, image_pos, counts);
   if (a.n > 0) hipLaunchKernelGGL(splice_gather_kernel, dim3(row_blocks(a.n)), dim3(256), 0, stream, a);

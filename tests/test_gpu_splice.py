@@ -113,6 +113,43 @@ def test_forward_backward(shape, padding_idx, dtype):
         assert np.array_equal(out.float().detach().cpu().numpy(), ow)
 
 
+@pytest.mark.parametrize("n", [1, 100, 20000, 32768, 32769, 40000])
+@pytest.mark.parametrize("vis_rows", ["fewer", "equal", "more"])
+def test_raw_outputs_both_launch_paths(n, vis_rows):
+    """The raw call's three outputs against numpy: up to 32768 tokens one
+    kernel counts the image tokens per workgroup, above that a one-workgroup
+    scan runs first.  Rows of image tokens past the vision rows and of ids
+    outside [0, vocab) are zero; image_pos holds each vision row's token and
+    -1 for rows no token took; counts = (image tokens, bad ids)."""
+    print(f"splice raw n={n} vision rows {vis_rows}", flush=True)
+    g = torch.Generator().manual_seed(n)
+    vocab, hidden = 256, 64
+    ids = torch.randint(0, vocab, (n,), generator=g)
+    ids[ids == IMG] = 1
+    n_img = n // 5
+    ids[torch.randperm(n, generator=g)[:n_img]] = IMG
+    if n > 1:
+        ids[torch.randperm(n, generator=g)[:3]] = torch.tensor([-4, vocab, vocab + 77])[: min(3, n)]
+    found = int((ids == IMG).sum())
+    nv = {"fewer": max(found - 7, 0), "equal": found, "more": found + 11}[vis_rows]
+    weight = torch.randn(vocab, hidden, generator=g).to(torch.bfloat16)
+    vis = torch.randn(nv, hidden, generator=g).to(torch.bfloat16)
+    out, image_pos, counts = S.splice_fwd(ids.to(DEV), weight.to(DEV), vis.to(DEV), IMG)
+    torch.cuda.synchronize()
+    idn = ids.numpy()
+    want = np.zeros((n, hidden), np.float32)
+    ok = (idn >= 0) & (idn < vocab) & (idn != IMG)
+    want[ok] = weight.float().numpy()[idn[ok]]
+    pos = np.nonzero(idn == IMG)[0]
+    k = min(len(pos), nv)
+    want[pos[:k]] = vis.float().numpy()[:k]
+    want_pos = np.full(nv, -1, np.int64)
+    want_pos[:k] = pos[:k]
+    assert np.array_equal(out.float().cpu().numpy(), want)
+    assert np.array_equal(image_pos.cpu().numpy().astype(np.int64), want_pos)
+    assert counts.cpu().tolist() == [found, int(((idn < 0) | (idn >= vocab)).sum())]
+
+
 def test_count_mismatch_and_bad_ids():
     ids, emb, vis = make(2, 50, 256, 64, 10)
     with pytest.raises(ValueError, match="Shape Mismatch"):
