@@ -147,7 +147,7 @@ __device__ __forceinline__ bool plan_matches(const AttnParams& p, bool causal, b
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,
                            int causal, int n_rep, int hkv, PlanHeader* plan, SeqInfo* seq, QTile* qtiles, int qrows,
                            int qcap, KvItem* kvitems, int kvcap, int* seqbuf, SplitTile* splits, int* nsplit,
-                           hipStream_t stream);
+                           int* qfirst, hipStream_t stream);
 hipError_t launch_attn_fwd(const AttnParams& p, int d, int causal, int qcap, hipStream_t stream);
 hipError_t launch_attn_bwd(const AttnParams& p, int d, int causal, int qcap, int kvcap, hipStream_t stream);
 

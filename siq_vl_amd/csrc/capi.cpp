@@ -61,6 +61,8 @@ PlanLayout plan_layout(int batch, int64_t total_q, int64_t total_k, bool kv) {
   if (kv) off += align256(sizeof(siq::SplitTile) * (size_t)siq::kMaxSplitTiles);
   L.nsplit = off;
   if (kv) off += 256;
+  L.qfirst = off;
+  off += align256(sizeof(int) * ((size_t)(batch > 0 ? batch : 1) + 1));
   L.total = off;
   return L;
 }
@@ -97,7 +99,8 @@ hipError_t build_plan(char* base, const PlanLayout& L, const int32_t* cu_q, cons
                               kv ? reinterpret_cast<siq::KvItem*>(base + L.kvitems) : nullptr, L.kvcap,
                               kv ? reinterpret_cast<int*>(base + L.seqbuf) : nullptr,
                               kv ? reinterpret_cast<siq::SplitTile*>(base + L.splits) : nullptr,
-                              kv ? reinterpret_cast<int*>(base + L.nsplit) : nullptr, s);
+                              kv ? reinterpret_cast<int*>(base + L.nsplit) : nullptr,
+                              reinterpret_cast<int*>(base + L.qfirst), s);
 }
 
 int check_attn_common(int batch, int max_q, int max_k, int64_t total_q, int64_t total_k, int hq, int hkv, int d,

@@ -13,10 +13,12 @@ int ok();
 bool aligned16(const void* p);
 
 // An attention plan: header, per-sequence extents, the q-tile list (forward,
-// dQ) and the dK/dV work items with their split tiles.  It depends on the
-// sequences, the head counts and causality, not on the tensors.
+// dQ) and the dK/dV work items with their split tiles, and the scheduler's
+// per-sequence prefix buffers (used for batches too long for its LDS).  It
+// depends on the sequences, the head counts and causality, not on the
+// tensors.
 struct PlanLayout {
-  size_t header, seq, qtiles, kvitems, seqbuf, splits, nsplit, total;
+  size_t header, seq, qtiles, kvitems, seqbuf, splits, nsplit, qfirst, total;
   int qcap, kvcap;
 };
 

@@ -8,6 +8,9 @@
 // out of bounds, and writes the work lists ordered by decreasing work with a
 // counting sort.  The attention kernels then map blockIdx.x -> work.
 //
+// Both blocks read cu_seqlens once, into LDS.  Each sorts a flattened list of
+// tiles (a prefix over the sequences' tile counts maps tile i back to its
+// sequence), one tile per thread, so a long sequence is no serial loop.
 // Block 0 builds the q-tile list of the forward and dQ kernels (tiles of
 // `qrows` rows), heaviest first (work key: kv rows seen, in units of 64).  Block 1 builds the dK/dV
 // work items: a kv tile has n_rep x (q blocks that can see it) steps; tiles
@@ -119,6 +122,11 @@ __device__ int scan_global(int* a, int n, int* buf, int* wsum) {
   return carry;
 }
 
+// Sequence extents of the batch, read from cu_seqlens once into LDS (batches
+// of up to kSeqLds sequences; longer ones read them from global memory at each
+// use).
+constexpr int kSeqLds = 1024;
+
 __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __restrict__ cu_q,
                                                                  const int* __restrict__ cu_k, int batch,
                                                                  int64_t total_q, int64_t total_k, int causal,
@@ -128,12 +136,17 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
                                                                  KvItem* __restrict__ kvitems, int kvcap,
                                                                  int* __restrict__ seqbuf,
                                                                  SplitTile* __restrict__ splits,
-                                                                 int* __restrict__ nsplit) {
+                                                                 int* __restrict__ nsplit, int* __restrict__ qfirst) {
   __shared__ int hist[kSchedKeys];
   __shared__ int wsum[kSchedThreads / 64 + 1];
   __shared__ long long wsteps[kSchedThreads / 64];
   __shared__ int nslot, nsplit_sh, status_sh;
+  __shared__ SeqInfo seq_sh[kSeqLds];
+  // [batch + 1] first flattened tile (q tiles in block 0, kv tiles in block 1)
+  // of each sequence: in LDS when it fits, else in qfirst / seqbuf
+  __shared__ int tfirst_sh[kSchedKeys];
   const int tid = threadIdx.x;
+  const bool seq_lds = batch <= kSeqLds;
 
   for (int i = tid; i < kSchedKeys; i += kSchedThreads) hist[i] = 0;
   if (tid == 0) {
@@ -141,26 +154,54 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
     nsplit_sh = 0;
     status_sh = 0;
   }
-  __syncthreads();
-
-  if (blockIdx.x == 0) {
-    // q tiles of the forward / dQ kernels, heaviest first
+  if (seq_lds) {
     for (int b = tid; b < batch; b += kSchedThreads) {
       const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
-      seq[b] = s;
-      const int nt = (s.q_len + qrows - 1) / qrows;
-      for (int t = 0; t < nt; ++t) atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(s, t, qrows, causal)], 1);
+      seq_sh[b] = s;
+      if (blockIdx.x == 0) seq[b] = s;
+    }
+  } else if (blockIdx.x == 0) {
+    for (int b = tid; b < batch; b += kSchedThreads) seq[b] = seq_extent(cu_q, cu_k, b, total_q, total_k);
+  }
+  __syncthreads();
+  auto seq_of = [&](int b) { return seq_lds ? seq_sh[b] : seq_extent(cu_q, cu_k, b, total_q, total_k); };
+  int* tfirst = batch + 1 <= kSchedKeys ? tfirst_sh : (blockIdx.x == 0 ? qfirst : seqbuf);
+  // flattened tile i -> (sequence, tile): last b with tfirst[b] <= i
+  auto locate = [&](int i, int& b, int& t) {
+    int lo = 0, hi = batch - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tfirst[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    b = lo;
+    t = i - tfirst[lo];
+  };
+
+  if (blockIdx.x == 0) {
+    // q tiles of the forward / dQ kernels, heaviest first: a counting sort over
+    // the flattened tiles (one tile per thread and pass)
+    for (int b = tid; b < batch; b += kSchedThreads) tfirst[b] = (seq_of(b).q_len + qrows - 1) / qrows;
+    __threadfence_block();
+    __syncthreads();
+    const int ntiles = scan_global(tfirst, batch, hist, wsum);
+    if (tid == 0) tfirst[batch] = ntiles;
+    for (int i = tid; i < kSchedKeys; i += kSchedThreads) hist[i] = 0;
+    __threadfence_block();
+    __syncthreads();
+    for (int i = tid; i < ntiles; i += kSchedThreads) {
+      int b, t;
+      locate(i, b, t);
+      atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(seq_of(b), t, qrows, causal)], 1);
     }
     __syncthreads();
     const int total = block_exclusive_scan(hist, kSchedKeys, wsum);
-    for (int b = tid; b < batch; b += kSchedThreads) {
-      const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
-      const int nt = (s.q_len + qrows - 1) / qrows;
-      for (int t = 0; t < nt; ++t) {
-        const int pos = atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(s, t, qrows, causal)], 1);
-        if (pos < qcap) qtiles[pos] = QTile{s, b, t, 0, 0};
-        else atomicOr(&status_sh, kStatusOverflow);
-      }
+    for (int i = tid; i < ntiles; i += kSchedThreads) {
+      int b, t;
+      locate(i, b, t);
+      const SeqInfo s = seq_of(b);
+      const int pos = atomicAdd(&hist[kSchedKeys - 1 - q_tile_key(s, t, qrows, causal)], 1);
+      if (pos < qcap) qtiles[pos] = QTile{s, b, t, 0, 0};
+      else atomicOr(&status_sh, kStatusOverflow);
     }
     for (int i = total + tid; i < qcap; i += kSchedThreads) qtiles[i] = QTile{SeqInfo{0, 0, 0, 0}, -1, -1, 0, 0};
     __syncthreads();
@@ -198,13 +239,10 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
   }
 
   // dK/dV work items.  1: kv tiles per sequence (prefix sums) and the total
-  // number of steps (per kv-head).  The prefix array lives in LDS when it
-  // fits (no global write / read-back between the passes), else in seqbuf.
-  __shared__ int tfirst_sh[kSchedKeys];
-  int* tfirst = batch + 1 <= kSchedKeys ? tfirst_sh : seqbuf;  // [batch + 1] first flattened kv tile of each sequence
+  // number of steps (per kv-head).
   long long mine = 0;
   for (int b = tid; b < batch; b += kSchedThreads) {
-    const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
+    const SeqInfo s = seq_of(b);
     const int nt = (s.k_len + kBwdBN - 1) / kBwdBN;
     tfirst[b] = nt;
     for (int t = 0; t < nt; ++t) mine += kv_tile_steps(s, t, causal, n_rep);
@@ -235,22 +273,11 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
   if (sl < kMinSplitSteps) sl = kMinSplitSteps;
   if (sl > (1 << 30)) sl = 1 << 30;
   const int S = (int)sl;
-  // flattened tile i -> (sequence, tile): last b with tfirst[b] <= i
-  auto locate = [&](int i, int& b, int& t) {
-    int lo = 0, hi = batch - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (tfirst[mid] <= i) lo = mid; else hi = mid - 1;
-    }
-    b = lo;
-    t = i - tfirst[lo];
-  };
   // 3: counting sort of the pieces by steps, heaviest first
   for (int i = tid; i < ntiles; i += kSchedThreads) {
     int b, t;
     locate(i, b, t);
-    const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
-    const int w = kv_tile_steps(s, t, causal, n_rep);
+    const int w = kv_tile_steps(seq_of(b), t, causal, n_rep);
     const int np = w > S ? (w + S - 1) / S : 1;
     for (int pc = 0; pc < np; ++pc) atomicAdd(&hist[kSchedKeys - 1 - clamp_key(min(S, w - pc * S))], 1);
   }
@@ -260,7 +287,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
   for (int i = tid; i < ntiles; i += kSchedThreads) {
     int b, t;
     locate(i, b, t);
-    const SeqInfo s = seq_extent(cu_q, cu_k, b, total_q, total_k);
+    const SeqInfo s = seq_of(b);
     const int w = kv_tile_steps(s, t, causal, n_rep);
     const int np = w > S ? (w + S - 1) / S : 1;
     int slot0 = -1;
@@ -303,11 +330,11 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int* __re
 hipError_t launch_schedule(const int* cu_q, const int* cu_k, int batch, int64_t total_q, int64_t total_k,
                            int causal, int n_rep, int hkv, PlanHeader* plan, SeqInfo* seq, QTile* qtiles, int qrows,
                            int qcap, KvItem* kvitems, int kvcap, int* seqbuf, SplitTile* splits, int* nsplit,
-                           hipStream_t stream) {
+                           int* qfirst, hipStream_t stream) {
   const int blocks = kvitems != nullptr ? 2 : 1;
   hipLaunchKernelGGL(schedule_kernel, dim3(blocks), dim3(kSchedThreads), 0, stream, cu_q, cu_k, batch, total_q,
                      total_k, causal, n_rep, hkv, plan, seq, qtiles, qrows, qcap, kvitems, kvcap, seqbuf, splits,
-                     nsplit);
+                     nsplit, qfirst);
   return hipGetLastError();
 }
 
