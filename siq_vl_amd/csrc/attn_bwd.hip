@@ -1068,8 +1068,8 @@ hipError_t launch_bwd_t(const AttnParams& p, int qcap, int kvcap, hipStream_t st
   else
     hipLaunchKernelGGL((attn_bwd_dq_kernel<D, CAUSAL, false>), qgrid, dim3(256), 0, stream, p);
   // D = 64: one wave per SIMD (K, V, dK, dV and both groups' S / dP fit the
-  // registers); D = 128: two waves per SIMD (one wave would hold K and V only
-  // by shuttling accumulators through AGPRs, which measured 5-7% slower)
+  // registers); D = 128: two waves per SIMD (one wave per SIMD measured 5-10%
+  // slower with the accumulators or with K and V in AGPRs)
   if constexpr (D == 64)
     hipLaunchKernelGGL((attn_bwd_dkdv_w4_kernel<D, CAUSAL>), kvgrid, dim3(256), 0, stream, p);
   else
