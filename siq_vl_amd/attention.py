@@ -273,6 +273,15 @@ def varlen_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlen
 # that forms dQ in the dK/dV kernel and sums it with fp32 atomics.
 DETERMINISTIC_DEFAULT = True
 
+# flash-attention's ``deterministic=False`` (what transformers passes unless
+# FLASH_ATTENTION_DETERMINISTIC=1) permits a non-deterministic backward; it
+# does not ask for one.  On MI355X the deterministic backward is also the
+# faster one (2.0-3.1x over the atomic-dQ backward at the BASELINE shapes), so
+# ``flash_attn_varlen_func(..., deterministic=False)`` takes it too unless this
+# is set.  ``varlen_attn_bwd(deterministic=False)`` and the C ABI's
+# deterministic = 0 always run the atomic-dQ backward.
+ATOMIC_BACKWARD_ON_FALSE = False
+
 
 def varlen_attn_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
                     lse: torch.Tensor, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
@@ -516,8 +525,9 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu
     """Varlen attention with the flash-attention varlen call convention.
 
     ``q [total_q, hq, d]``, ``k/v [total_k, hkv, d]`` (bf16); returns ``[total_q, hq, d]``.
-    ``deterministic`` picks the backward (None: ``DETERMINISTIC_DEFAULT``).
-    Features outside the reference path (dropout, sliding window, softcap,
+    ``deterministic`` picks the backward (None: ``DETERMINISTIC_DEFAULT``;
+    False: the deterministic one as well, the faster here, unless
+    ``ATOMIC_BACKWARD_ON_FALSE``).  Features outside the reference path (dropout, sliding window, softcap,
     ALiBi, returning probabilities) are rejected, not approximated.
     """
     if dropout_p:
@@ -532,8 +542,9 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu
         raise ValueError("attention probabilities are never materialised")
     if softmax_scale is None:
         softmax_scale = q.shape[-1] ** -0.5
+    det = None if deterministic is None else (bool(deterministic) or not ATOMIC_BACKWARD_ON_FALSE)
     return _VarlenAttnFn.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), int(max_seqlen_k),
-                               float(softmax_scale), bool(causal), None if deterministic is None else bool(deterministic))
+                               float(softmax_scale), bool(causal), det)
 
 
 # --------------------------------------------------------------------------- transformers plug-in

@@ -13,7 +13,9 @@ the C ABI): dQ = dS K formed in the dK/dV kernel and summed with fp32 atomics.
 * no leakage across sequences (the atomics address only the step's own rows);
 * full BASELINE sizes (configs 2, 3, 5) against the per-sequence fp32 torch
   reference;
-* the autograd op's ``deterministic`` flag selects it.
+* the autograd op's ``deterministic=False`` selects it when
+  ``ATOMIC_BACKWARD_ON_FALSE`` is set, and otherwise takes the deterministic
+  (faster) backward, bit for bit.
 """
 
 import numpy as np
@@ -89,17 +91,41 @@ def test_atomic_no_cross_sequence_leakage():
         assert torch.equal(base["dk"][s:e], pert["dk"][s:e]) and torch.equal(base["dv"][s:e], pert["dv"][s:e])
 
 
-def test_autograd_flag_selects_the_atomic_backward():
+def _autograd_grads(q, k, v, do, cug, det):
+    xq, xk, xv = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    out = A.flash_attn_varlen_func(xq, xk, xv, cug, cug, 300, 300, causal=True, deterministic=det)
+    out.backward(do.to(DEV))
+    return xq.grad.cpu(), xk.grad.cpu(), xv.grad.cpu()
+
+
+def test_autograd_flag_selects_the_atomic_backward(monkeypatch):
     q, k, v, do, cu = make([40, 300, 7], 12, 2, 128, seed=4)
     cug = cu.to(DEV)
-    grads = {}
-    for det in (True, False):
-        xq, xk, xv = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
-        out = A.flash_attn_varlen_func(xq, xk, xv, cug, cug, 300, 300, causal=True, deterministic=det)
-        out.backward(do.to(DEV))
-        grads[det] = (xq.grad.float().cpu().numpy(), xk.grad.cpu(), xv.grad.cpu())
+    monkeypatch.setattr(A, "ATOMIC_BACKWARD_ON_FALSE", True)
+    grads = {det: _autograd_grads(q, k, v, do, cug, det) for det in (True, False)}
     assert torch.equal(grads[True][1], grads[False][1]) and torch.equal(grads[True][2], grads[False][2])
-    assert rel(grads[False][0], grads[True][0]) <= 1e-2
+    assert rel(grads[False][0].float().numpy(), grads[True][0].float().numpy()) <= 1e-2
+    # the atomic-dQ backward really ran: the low-level call with deterministic=False gives its dq bits
+    scale = q.shape[-1] ** -0.5
+    qg, kg, vg, dog = (t.to(DEV) for t in (q, k, v, do))
+    out, lse = A.varlen_attn_fwd(qg, kg, vg, cug, cug, 300, 300, scale, True)
+    dq_atomic = A.varlen_attn_bwd(dog, qg, kg, vg, out, lse, cug, cug, 300, 300, scale, True, deterministic=False)[0]
+    dq_det = A.varlen_attn_bwd(dog, qg, kg, vg, out, lse, cug, cug, 300, 300, scale, True, deterministic=True)[0]
+    assert rel(grads[False][0].float().numpy(), dq_atomic.float().cpu().numpy()) <= 1e-2
+    assert torch.equal(grads[True][0], dq_det.cpu())
+
+
+def test_autograd_false_takes_the_deterministic_backward_by_default():
+    """flash-attention's deterministic=False (transformers' default) permits
+    either backward; the deterministic one, the faster here, runs: the
+    gradients are bitwise those of deterministic=True."""
+    assert A.ATOMIC_BACKWARD_ON_FALSE is False
+    q, k, v, do, cu = make([40, 300, 7], 12, 2, 128, seed=5)
+    cug = cu.to(DEV)
+    g_true = _autograd_grads(q, k, v, do, cug, True)
+    g_false = _autograd_grads(q, k, v, do, cug, False)
+    for a, b in zip(g_true, g_false):
+        assert torch.equal(a, b)
 
 
 @pytest.mark.slow
