@@ -110,3 +110,15 @@ def test_many_tiny_sequences(d, causal):
     lengths = [int(x) for x in g.integers(0, 25, size=700)]
     lengths.insert(350, 900)
     check(lengths, lengths, 4, 2, d, causal, seed=6)
+
+
+@pytest.mark.parametrize("d,causal", [(64, True), (128, False)])
+def test_more_sequences_than_the_scheduler_lds_holds(d, causal):
+    # 2600 sequences of 0..6 tokens and one of 700: past 1024 sequences the
+    # scheduler reads the extents from cu_seqlens at each use instead of from
+    # LDS, and past 2047 its per-sequence tile prefixes live in the plan's
+    # global buffers instead of LDS
+    g = np.random.default_rng(23)
+    lengths = [int(x) for x in g.integers(0, 7, size=2600)]
+    lengths.insert(1300, 700)
+    check(lengths, lengths, 4, 2, d, causal, seed=7)
