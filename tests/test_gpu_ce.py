@@ -58,6 +58,21 @@ def test_small_vs_oracle(chunk):
     assert np.all(dh[ignored.numpy()] == 0.0)
 
 
+@pytest.mark.parametrize("hdim,vocab", [(896, 2000), (320, 1000)])
+def test_hidden_sizes_off_the_tile_grid(hdim, vocab):
+    """hdim 896 (Qwen2.5-0.5B: three whole 256-wide tiles of the gradient
+    GEMMs and a half one) and 320 (one whole tile and a quarter), with a
+    vocabulary that ends inside a tile, over three chunks."""
+    h, w, y = make(300, hdim, vocab, seed=31)
+    print(f"flce hdim={hdim} V={vocab}", flush=True)
+    loss, count, bad, dh, dw = run(h, w, y, 128)
+    ref = oc.linear_ce(h, w, y)
+    assert count == ref["count"] and bad == 0
+    assert abs(loss - ref["loss"]) <= TOL * abs(ref["loss"])
+    assert rel(dh, ref["dh"]) <= TOL and rel(dw, ref["dw"]) <= TOL
+    assert np.all(dh[(y == -100).numpy()] == 0.0)
+
+
 def test_sum_reduction_with_divisor():
     h, w, y = make(200, 128, 520, seed=2)
     loss, count, _, dh, dw = run(h, w, y, 64, divisor=517.0)
