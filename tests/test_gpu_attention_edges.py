@@ -122,3 +122,9 @@ def test_more_sequences_than_the_scheduler_lds_holds(d, causal):
     lengths = [int(x) for x in g.integers(0, 7, size=2600)]
     lengths.insert(1300, 700)
     check(lengths, lengths, 4, 2, d, causal, seed=7)
+
+
+@pytest.mark.parametrize("hq,hkv", [(28, 4), (40, 8)])
+def test_larger_qwen_head_layouts(hq, hkv):
+    # Qwen2.5-7B (28 / 4 heads) and -14B (40 / 8) at d 128: GQA groups of 7 and 5, several kv-heads
+    check([257, 40, 611, 128], [257, 40, 611, 128], hq, hkv, 128, True, seed=8)
